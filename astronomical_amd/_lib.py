@@ -1,0 +1,115 @@
+"""ctypes binding of include/astro_moe.h (libastro_moe.so, built in-tree).
+
+The product path is the HIP library only: if it is missing, loading raises — there is
+no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libastro_moe.so")
+
+OK, INVALID_ARGUMENT, UNSUPPORTED, WORKSPACE_TOO_SMALL, HIP_ERROR = 0, 1, 2, 3, 4
+
+
+class AstroMoeError(RuntimeError):
+    """A failed C-ABI call: status code and the library's thread-local message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+        self.message = message
+
+
+class Affine(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("experts", C.c_int32), ("out_features", C.c_int32), ("in_features", C.c_int32),
+                ("bits", C.c_int32), ("group_size", C.c_int32)]
+
+
+class Layer(C.Structure):
+    _fields_ = [("hidden", C.c_int32), ("num_experts", C.c_int32), ("top_k", C.c_int32),
+                ("intermediate", C.c_int32), ("shared_intermediate", C.c_int32),
+                ("normalize_top_k", C.c_int32), ("router_w", C.c_void_p), ("router_q", Affine),
+                ("router_bias", C.c_void_p), ("gate_up", Affine), ("gate", Affine), ("up", Affine),
+                ("down", Affine), ("shared_gate", Affine), ("shared_up", Affine),
+                ("shared_down", Affine), ("shared_expert_gate", Affine),
+                ("slot_of_expert", C.c_void_p)]
+
+
+class WorkspaceView(C.Structure):
+    _fields_ = [("total_bytes", C.c_size_t), ("sorted_path", C.c_int32)] + [
+        (n, C.c_size_t) for n in ("logits", "indices", "scores", "sorted_order", "inverse_order",
+                                  "sorted_ids", "expert_offsets", "activated", "expert_out",
+                                  "sparse", "shared_out", "shared_gate_logits")]
+
+
+EXPORTS = {
+    # name: (argtypes, restype)
+    "astro_moe_last_error": ([], C.c_char_p),
+    "astro_moe_abi_version": ([], C.c_int),
+    "astro_moe_workspace_bytes": ([C.POINTER(Layer), C.c_int32, C.POINTER(C.c_size_t)], C.c_int),
+    "astro_moe_workspace_layout": ([C.POINTER(Layer), C.c_int32, C.POINTER(WorkspaceView)], C.c_int),
+    "astro_moe_block_forward": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                                 C.c_size_t, C.c_void_p], C.c_int),
+    "astro_moe_router_logits": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_route_topk": ([C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
+                              C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_sort_workspace_bytes": ([C.c_int32, C.c_int32, C.POINTER(C.c_size_t)], C.c_int),
+    "astro_moe_sort_assignments": ([C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
+                                    C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "astro_moe_invert_assignment_order": ([C.c_void_p, C.c_int32, C.c_void_p], C.c_int),
+    "astro_moe_gather_qmm_workspace_bytes": ([C.c_int32, C.c_int32, C.POINTER(C.c_size_t)], C.c_int),
+    "astro_moe_gather_qmm": ([C.c_void_p, C.c_void_p, C.c_int32, C.POINTER(Affine), C.c_void_p,
+                              C.c_int32, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "astro_moe_quantized_matmul": ([C.c_void_p, C.c_int32, C.POINTER(Affine), C.c_void_p,
+                                    C.c_void_p], C.c_int),
+    "astro_moe_swiglu": ([C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_sorted_weighted_sum": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                       C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_unsorted_weighted_sum": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                         C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_combine_shared": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                  C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_shared_expert_workspace_bytes": ([C.POINTER(Layer), C.c_int32,
+                                                 C.POINTER(C.c_size_t)], C.c_int),
+    "astro_moe_shared_expert": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                                 C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "astro_synth_words": ([C.c_void_p, C.c_int64, C.c_uint64, C.c_void_p], C.c_int),
+    "astro_synth_uniform_bf16": ([C.c_void_p, C.c_int64, C.c_uint64, C.c_double, C.c_double,
+                                  C.c_void_p], C.c_int),
+    "astro_synth_affine_biases": ([C.c_void_p, C.c_void_p, C.c_int64, C.c_uint64, C.c_double,
+                                   C.c_double, C.c_void_p], C.c_int),
+    "astro_synth_normal_bf16": ([C.c_void_p, C.c_int64, C.c_uint64, C.c_double, C.c_void_p], C.c_int),
+    "astro_synth_activations": ([C.c_void_p, C.c_int32, C.c_int32, C.c_uint64, C.c_void_p], C.c_int),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libastro_moe.so; raises if it has not been built (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
+                               "(python -m astronomical_amd.build) first")
+        L = C.CDLL(LIB_PATH)
+        for name, (args, res) in EXPORTS.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != OK:
+        msg = lib().astro_moe_last_error().decode(errors="replace")
+        raise AstroMoeError(status, msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))

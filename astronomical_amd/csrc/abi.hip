@@ -1,0 +1,617 @@
+// Host layer of the C ABI: argument validation (mirroring the reference's checks and
+// messages), the workspace layout, and the launch sequence of the block.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/astro_moe.h"
+#include "kernels.h"
+
+using namespace astro;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char *op, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = std::string(op) + ": " + buf;
+  return status;
+}
+
+int ok() {
+  g_last_error.clear();
+  return ASTRO_MOE_OK;
+}
+
+int hip_fail(const char *op, hipError_t e) {
+  return fail(ASTRO_MOE_HIP_ERROR, op, "HIP error %d (%s)", (int)e, hipGetErrorString(e));
+}
+
+// The marker keeps classify_mlx_error (error_handling.rs:81-122) classifying the failure
+// as ActiveMemoryLimitExceeded; only key=value fields may follow it.
+int workspace_fail(const char *op, size_t need, size_t have) {
+  return fail(ASTRO_MOE_WORKSPACE_TOO_SMALL, op,
+              "ASTRONOMICAL_MLX_ACTIVE_MEMORY_LIMIT_EXCEEDED active_bytes=0 allocation_bytes=%zu "
+              "allowed_bytes=%zu",
+              need, have);
+}
+
+const char *const kBlockOp = "run the Qwen3.5-MoE sparse expert block";
+const char *const kRouteOp = "route Qwen3.5-MoE sparse experts";           // routing.rs:11
+const char *const kSortOp = "sort stacked expert assignments";             // assignment_sort.rs:10
+const char *const kReduceOp = "reduce stacked expert outputs";             // weighted_sum.rs:15
+const char *const kCombineOp = "combine Qwen3.5-MoE sparse and shared experts";  // routing.rs:12
+const char *const kGatherOp = "build affine gather_qmm";                  // mlx_quantized_operations.rs:114
+const char *const kQmmOp = "build affine quantized matmul";               // mlx_quantized_operations.rs:60
+const char *const kPermOp = "invert assignment permutation";
+
+// validate_affine_quantized_matmul_arguments (mlx_quantized_operations.rs:226-330), then
+// what the gfx950 kernels implement.
+int check_affine(const char *op, const astro_moe_affine *w, int inner) {
+  if (!w || !w->w || !w->scales || !w->biases)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "affine weights, scales and biases must be non-null");
+  if (w->group_size != 32 && w->group_size != 64 && w->group_size != 128)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "affine group size must be 32, 64, or 128");
+  if (w->bits != 2 && w->bits != 3 && w->bits != 4 && w->bits != 5 && w->bits != 6 && w->bits != 8)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "affine bit width must be 2, 3, 4, 5, 6, or 8");
+  if (w->experts <= 0 || w->out_features <= 0 || w->in_features <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "array shape must have a positive tail dimension");
+  if (((int64_t)w->in_features * w->bits) % 32 != 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op,
+                "packed weight shape overflows or is incompatible with the requested bit width");
+  if (w->in_features % w->group_size != 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op,
+                "affine scale and bias shapes do not match the packed weight shape");
+  if (inner >= 0 && inner != w->in_features)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op,
+                "activation inner dimension does not match the expanded quantized weight input");
+  if (w->bits != 4 && w->bits != 8)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "the gfx950 kernels implement 4-bit and 8-bit affine weights");
+  if (w->in_features % 64 != 0)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "the gfx950 kernels need an input width that is a multiple of 64");
+  return ASTRO_MOE_OK;
+}
+
+int64_t words_per_row(const astro_moe_affine &w) { return (int64_t)w.in_features * w.bits / 32; }
+int64_t groups_per_row(const astro_moe_affine &w) { return w.in_features / w.group_size; }
+
+// Fill the weight part of a GemmArgs from one projection (or a gate/up pair).
+void set_weights(GemmArgs &g, const astro_moe_affine &gate, const astro_moe_affine *up,
+                 int64_t up_row_offset) {
+  g.bkind = gate.bits == 8 ? kBQ8 : kBQ4;
+  g.group = gate.group_size;
+  g.w_row_stride = words_per_row(gate);
+  g.sb_row_stride = groups_per_row(gate);
+  g.w_expert_stride = (int64_t)gate.out_features * g.w_row_stride;
+  g.sb_expert_stride = (int64_t)gate.out_features * g.sb_row_stride;
+  g.w0 = gate.w;
+  g.s0 = gate.scales;
+  g.b0 = gate.biases;
+  if (up) {
+    g.w1 = up->w + up_row_offset * g.w_row_stride;
+    g.s1 = up->scales + up_row_offset * g.sb_row_stride;
+    g.b1 = up->biases + up_row_offset * g.sb_row_stride;
+  }
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct Layout {
+  size_t logits, idx, scores, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
+      tile_count, act, eout, sparse, shared_act, shared_out, z, total;
+  int max_tiles;
+};
+
+Layout block_layout(const astro_moe_layer &L, int T) {
+  Layout o{};
+  const size_t A = (size_t)T * L.top_k, E = (size_t)L.num_experts;
+  o.max_tiles = sort_max_tiles((int)A, (int)E);
+  size_t p = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = p;
+    p = align_up(p + bytes);
+    return at;
+  };
+  o.logits = take((size_t)T * E * 2);
+  o.idx = take(A * 4);
+  o.scores = take(A * 2);
+  o.sorted_order = take(A * 4);
+  o.inverse = take(A * 4);
+  o.sorted_ids = take(A * 4);
+  o.offsets = take((E + 2) * 4);
+  o.tile_expert = take((size_t)o.max_tiles * 4);
+  o.tile_row0 = take((size_t)o.max_tiles * 4);
+  o.tile_count = take(4);
+  o.act = take(A * (size_t)L.intermediate * 2);
+  o.eout = take(A * (size_t)L.hidden * 2);
+  o.sparse = take((size_t)T * L.hidden * 2);
+  const size_t Is = L.shared_intermediate > 0 ? (size_t)L.shared_intermediate : 0;
+  o.shared_act = take((size_t)T * Is * 2);
+  o.shared_out = take(Is ? (size_t)T * L.hidden * 2 : 0);
+  o.z = take(Is ? (size_t)T * 2 : 0);
+  o.total = p;
+  return o;
+}
+
+int check_layer(const char *op, const astro_moe_layer *L) {
+  if (!L) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "layer description must be non-null");
+  const int H = L->hidden, E = L->num_experts, k = L->top_k, I = L->intermediate;
+  if (H <= 0 || E <= 0 || I <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "hidden, expert and intermediate sizes must be positive");
+  if (k <= 0 || k > E)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op,
+                "selected expert count must be positive and no larger than the router dimension");
+  if (E > 1024 || k > 64)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "the router kernel supports at most 1024 experts and top-64");
+  if (L->slot_of_expert)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "compact page slots are not implemented in this version");
+  if (!!L->router_w == !!L->router_q.w)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "exactly one of the dense and affine router weights must be set");
+  if (L->router_q.w) {
+    int rc = check_affine(op, &L->router_q, H);
+    if (rc) return rc;
+    if (L->router_q.experts != 1 || L->router_q.out_features != E)
+      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "router weights must map the hidden size to the expert count");
+  }
+  if (H % 64 != 0 || I % 64 != 0)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "the gfx950 kernels need hidden and intermediate sizes that are multiples of 64");
+  if (L->gate_up.w) {
+    int rc = check_affine(op, &L->gate_up, H);
+    if (rc) return rc;
+    if (L->gate_up.experts != E || L->gate_up.out_features != 2 * I)
+      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "resident fused gate/up output dimension must be twice the intermediate size");
+  } else {
+    int rc = check_affine(op, &L->gate, H);
+    if (!rc) rc = check_affine(op, &L->up, H);
+    if (rc) return rc;
+    if (L->gate.experts != E || L->up.experts != E || L->gate.out_features != I ||
+        L->up.out_features != I || L->gate.bits != L->up.bits || L->gate.group_size != L->up.group_size)
+      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "separate gate and up projections must share shape and quantization");
+  }
+  {
+    int rc = check_affine(op, &L->down, I);
+    if (rc) return rc;
+    if (L->down.experts != E || L->down.out_features != H)
+      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "down projection must map the intermediate size back to the hidden size");
+  }
+  if (L->shared_intermediate < 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "shared expert intermediate size must not be negative");
+  if (L->shared_intermediate > 0) {
+    const int Is = L->shared_intermediate;
+    int rc = check_affine(op, &L->shared_gate, H);
+    if (!rc) rc = check_affine(op, &L->shared_up, H);
+    if (!rc) rc = check_affine(op, &L->shared_down, Is);
+    if (!rc) rc = check_affine(op, &L->shared_expert_gate, H);
+    if (rc) return rc;
+    if (Is % 64 != 0)
+      return fail(ASTRO_MOE_UNSUPPORTED, op, "the gfx950 kernels need a shared intermediate size that is a multiple of 64");
+    if (L->shared_gate.out_features != Is || L->shared_up.out_features != Is ||
+        L->shared_down.out_features != H || L->shared_expert_gate.out_features != 1 ||
+        L->shared_gate.bits != L->shared_up.bits || L->shared_gate.group_size != L->shared_up.group_size)
+      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "shared expert projections have inconsistent shapes");
+  }
+  return ASTRO_MOE_OK;
+}
+
+hipError_t run_router(const astro_moe_layer &L, const uint16_t *x, int T, uint16_t *logits,
+                      hipStream_t s) {
+  GemmArgs g{};
+  g.A = x;
+  g.lda = L.hidden;
+  g.a_div = 1;
+  g.K = L.hidden;
+  g.N = L.num_experts;
+  g.M = T;
+  g.C = logits;
+  g.ldc = L.num_experts;
+  if (L.router_w) {
+    g.bkind = kBDense;
+    g.bd = L.router_w;
+    g.bd_row_stride = L.hidden;
+  } else {
+    set_weights(g, L.router_q, nullptr, 0);
+  }
+  g.bias = L.router_bias;
+  return launch_grouped_gemm(g, L.router_bias ? kEpiBias : kEpiPlain, s);
+}
+
+// shared expert: act = swiglu(gate(x), up(x)); out = down(act); z = shared_expert_gate(x)
+hipError_t run_shared(const astro_moe_layer &L, const uint16_t *x, int T, uint16_t *act,
+                      uint16_t *out, uint16_t *z, hipStream_t s) {
+  GemmArgs g{};
+  g.A = x;
+  g.lda = L.hidden;
+  g.a_div = 1;
+  g.K = L.hidden;
+  g.N = L.shared_intermediate;
+  g.M = T;
+  set_weights(g, L.shared_gate, &L.shared_up, 0);
+  g.w_expert_stride = g.sb_expert_stride = 0;
+  g.C = act;
+  g.ldc = L.shared_intermediate;
+  hipError_t e = launch_grouped_gemm(g, kEpiSwiglu, s);
+  if (e != hipSuccess) return e;
+  GemmArgs d{};
+  d.A = act;
+  d.lda = L.shared_intermediate;
+  d.a_div = 1;
+  d.K = L.shared_intermediate;
+  d.N = L.hidden;
+  d.M = T;
+  set_weights(d, L.shared_down, nullptr, 0);
+  d.C = out;
+  d.ldc = L.hidden;
+  e = launch_grouped_gemm(d, kEpiPlain, s);
+  if (e != hipSuccess) return e;
+  const astro_moe_affine &zg = L.shared_expert_gate;
+  return launch_qgemv_rows(x, T, L.hidden, zg.w, zg.scales, zg.biases, 1, zg.bits, zg.group_size,
+                           z, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *astro_moe_last_error(void) { return g_last_error.c_str(); }
+
+int astro_moe_abi_version(void) { return ASTRO_MOE_ABI_VERSION; }
+
+int astro_moe_workspace_bytes(const astro_moe_layer *layer, int32_t tokens, size_t *bytes) {
+  int rc = check_layer(kBlockOp, layer);
+  if (rc) return rc;
+  if (tokens < 0 || !bytes) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
+  *bytes = block_layout(*layer, tokens).total;
+  return ok();
+}
+
+int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
+                               astro_moe_workspace_view *view) {
+  int rc = check_layer(kBlockOp, layer);
+  if (rc) return rc;
+  if (tokens < 0 || !view) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
+  const Layout o = block_layout(*layer, tokens);
+  view->total_bytes = o.total;
+  view->sorted_path = (int64_t)tokens * layer->top_k >= 64;
+  view->logits = o.logits;
+  view->indices = o.idx;
+  view->scores = o.scores;
+  view->sorted_order = o.sorted_order;
+  view->inverse_order = o.inverse;
+  view->sorted_ids = o.sorted_ids;
+  view->expert_offsets = o.offsets;
+  view->activated = o.act;
+  view->expert_out = o.eout;
+  view->sparse = o.sparse;
+  view->shared_out = o.shared_out;
+  view->shared_gate_logits = o.z;
+  return ok();
+}
+
+int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                            uint16_t *y, void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = check_layer(kBlockOp, layer);
+  if (rc) return rc;
+  if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
+  if (tokens == 0) return ok();
+  if (!x || !y) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "hidden states and output must be non-null");
+  const astro_moe_layer &L = *layer;
+  const Layout o = block_layout(L, tokens);
+  if (!workspace || workspace_bytes < o.total) return workspace_fail(kBlockOp, o.total, workspace ? workspace_bytes : 0);
+  hipStream_t s = (hipStream_t)stream;
+  char *ws = (char *)workspace;
+  auto at = [&](size_t off) { return (void *)(ws + off); };
+  const int T = tokens, H = L.hidden, E = L.num_experts, k = L.top_k, I = L.intermediate;
+  const int A = T * k;
+  uint16_t *logits = (uint16_t *)at(o.logits);
+  uint32_t *idx = (uint32_t *)at(o.idx);
+  uint16_t *scores = (uint16_t *)at(o.scores);
+  uint32_t *sorted_order = (uint32_t *)at(o.sorted_order);
+  uint32_t *inverse = (uint32_t *)at(o.inverse);
+  uint32_t *sorted_ids = (uint32_t *)at(o.sorted_ids);
+  uint32_t *offsets = (uint32_t *)at(o.offsets);
+  uint32_t *tile_expert = (uint32_t *)at(o.tile_expert);
+  uint32_t *tile_row0 = (uint32_t *)at(o.tile_row0);
+  uint32_t *tile_count = (uint32_t *)at(o.tile_count);
+  uint16_t *act = (uint16_t *)at(o.act);
+  uint16_t *eout = (uint16_t *)at(o.eout);
+  uint16_t *sparse = (uint16_t *)at(o.sparse);
+
+  hipError_t e = run_router(L, x, T, logits, s);
+  if (e == hipSuccess) e = launch_route_topk(logits, T, E, k, L.normalize_top_k, idx, scores, s);
+  if (e == hipSuccess)
+    e = launch_sort(idx, A, E, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
+                    tile_count, s);
+  if (e != hipSuccess) return hip_fail(kBlockOp, e);
+
+  // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / k]
+  GemmArgs gu{};
+  gu.A = x;
+  gu.lda = H;
+  gu.a_rows = sorted_order;
+  gu.a_div = k;
+  gu.K = H;
+  gu.N = I;
+  if (L.gate_up.w)
+    set_weights(gu, L.gate_up, &L.gate_up, I);
+  else
+    set_weights(gu, L.gate, &L.up, 0);
+  gu.tile_expert = tile_expert;
+  gu.tile_row0 = tile_row0;
+  gu.tile_count = tile_count;
+  gu.expert_offsets = offsets;
+  gu.max_tiles = o.max_tiles;
+  gu.C = act;
+  gu.ldc = I;
+  e = launch_grouped_gemm(gu, kEpiSwiglu, s);
+
+  GemmArgs dn{};
+  dn.A = act;
+  dn.lda = I;
+  dn.a_div = 1;
+  dn.K = I;
+  dn.N = H;
+  set_weights(dn, L.down, nullptr, 0);
+  dn.tile_expert = tile_expert;
+  dn.tile_row0 = tile_row0;
+  dn.tile_count = tile_count;
+  dn.expert_offsets = offsets;
+  dn.max_tiles = o.max_tiles;
+  dn.C = eout;
+  dn.ldc = H;
+  if (e == hipSuccess) e = launch_grouped_gemm(dn, kEpiPlain, s);
+
+  const bool has_shared = L.shared_intermediate > 0;
+  uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
+  uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
+  if (e == hipSuccess && has_shared)
+    e = run_shared(L, x, T, (uint16_t *)at(o.shared_act), shared_out, z, s);
+  // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
+  if (e == hipSuccess)
+    e = launch_combine(eout, inverse, scores, T, k, H, A >= 64, shared_out, z, sparse, y, s);
+  if (e != hipSuccess) return hip_fail(kBlockOp, e);
+  return ok();
+}
+
+int astro_moe_router_logits(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                            uint16_t *logits, void *stream) {
+  int rc = check_layer(kRouteOp, layer);
+  if (rc) return rc;
+  if (tokens < 0 || (tokens > 0 && (!x || !logits)))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kRouteOp, "router inputs must be non-null");
+  if (tokens == 0) return ok();
+  hipError_t e = run_router(*layer, x, tokens, logits, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(kRouteOp, e);
+}
+
+int astro_moe_route_topk(const uint16_t *logits, int32_t tokens, int32_t experts, int32_t top_k,
+                         int32_t normalize, uint32_t *indices, uint16_t *scores, void *stream) {
+  // validate_router_arguments (routing.rs:123-153)
+  if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kRouteOp, "router logits must include token and expert dimensions");
+  if (experts <= 0 || top_k <= 0 || top_k > experts)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kRouteOp,
+                "selected expert count must be positive and no larger than the router dimension");
+  if (experts > 1024 || top_k > 64)
+    return fail(ASTRO_MOE_UNSUPPORTED, kRouteOp, "the router kernel supports at most 1024 experts and top-64");
+  if (tokens == 0) return ok();
+  if (!logits || !indices || !scores) return fail(ASTRO_MOE_INVALID_ARGUMENT, kRouteOp, "router buffers must be non-null");
+  hipError_t e = launch_route_topk(logits, tokens, experts, top_k, normalize, indices, scores,
+                                   (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(kRouteOp, e);
+}
+
+static size_t sort_ws_bytes(int A, int E) {
+  const int mt = sort_max_tiles(A, E);
+  return align_up(((size_t)E + 2) * 4) + 2 * align_up((size_t)mt * 4) + align_up(4);
+}
+
+int astro_moe_sort_workspace_bytes(int32_t assignments, int32_t experts, size_t *bytes) {
+  if (assignments < 0 || experts <= 0 || !bytes)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kSortOp, "expert assignments and expanded hidden states have invalid shapes");
+  *bytes = sort_ws_bytes(assignments, experts);
+  return ok();
+}
+
+int astro_moe_sort_assignments(const uint32_t *ids, int32_t assignments, int32_t experts,
+                               uint32_t *sorted_order, uint32_t *inverse_order,
+                               uint32_t *sorted_ids, uint32_t *expert_offsets, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  if (assignments < 0 || experts <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kSortOp, "expert assignments and expanded hidden states have invalid shapes");
+  const size_t need = sort_ws_bytes(assignments, experts);
+  if (!workspace || workspace_bytes < need) return workspace_fail(kSortOp, need, workspace ? workspace_bytes : 0);
+  if (assignments > 0 && (!ids || !sorted_order || !inverse_order || !sorted_ids))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kSortOp, "assignment buffers must be non-null");
+  hipStream_t s = (hipStream_t)stream;
+  char *ws = (char *)workspace;
+  const int mt = sort_max_tiles(assignments, experts);
+  uint32_t *off = (uint32_t *)ws;
+  uint32_t *te = (uint32_t *)(ws + align_up(((size_t)experts + 2) * 4));
+  uint32_t *tr = (uint32_t *)((char *)te + align_up((size_t)mt * 4));
+  uint32_t *tc = (uint32_t *)((char *)tr + align_up((size_t)mt * 4));
+  hipError_t e = launch_sort(ids, assignments, experts, sorted_order, inverse_order, sorted_ids,
+                             off, te, tr, tc, s);
+  if (e == hipSuccess && expert_offsets)
+    e = hipMemcpyAsync(expert_offsets, off, ((size_t)experts + 1) * 4, hipMemcpyDeviceToDevice, s);
+  return e == hipSuccess ? ok() : hip_fail(kSortOp, e);
+}
+
+int astro_moe_invert_assignment_order(const uint32_t *sorted_order, int32_t n,
+                                      uint32_t *inverse_order) {
+  if (n < 0 || (n > 0 && (!sorted_order || !inverse_order)))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kPermOp, "assignment permutation length exceeds u32");
+  std::vector<uint8_t> seen((size_t)n, 0);
+  for (int32_t s = 0; s < n; ++s) {
+    const uint32_t o = sorted_order[s];
+    if (o >= (uint32_t)n)
+      return fail(ASTRO_MOE_INVALID_ARGUMENT, kPermOp, "assignment permutation contains an out-of-range slot");
+    if (seen[o]) return fail(ASTRO_MOE_INVALID_ARGUMENT, kPermOp, "assignment permutation contains a duplicate slot");
+    seen[o] = 1;
+    inverse_order[o] = (uint32_t)s;
+  }
+  for (int32_t s = 0; s < n; ++s)
+    if (!seen[s]) return fail(ASTRO_MOE_INVALID_ARGUMENT, kPermOp, "assignment permutation is missing a slot");
+  return ok();
+}
+
+int astro_moe_gather_qmm_workspace_bytes(int32_t rows, int32_t experts, size_t *bytes) {
+  if (rows < 0 || experts <= 0 || !bytes)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kGatherOp, "gather_qmm requires at least one index array");
+  *bytes = 3 * align_up((size_t)rows * 4) + sort_ws_bytes(rows, experts);
+  return ok();
+}
+
+int astro_moe_gather_qmm(const uint16_t *x, const uint32_t *x_rows, int32_t rows,
+                         const astro_moe_affine *w, const uint32_t *ids, int32_t sorted_indices,
+                         uint16_t *out, void *workspace, size_t workspace_bytes, void *stream) {
+  (void)sorted_indices;  // a promise about id order; kernel selection here ignores it
+  int rc = check_affine(kGatherOp, w, -1);
+  if (rc) return rc;
+  if (rows < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kGatherOp, "activation and weight arrays must both have rank at least two");
+  if (rows == 0) return ok();
+  if (!x || !ids || !out) return fail(ASTRO_MOE_INVALID_ARGUMENT, kGatherOp, "gather_qmm requires at least one index array");
+  size_t need = 0;
+  astro_moe_gather_qmm_workspace_bytes(rows, w->experts, &need);
+  if (!workspace || workspace_bytes < need) return workspace_fail(kGatherOp, need, workspace ? workspace_bytes : 0);
+  hipStream_t s = (hipStream_t)stream;
+  char *ws = (char *)workspace;
+  const size_t ra = align_up((size_t)rows * 4);
+  uint32_t *so = (uint32_t *)ws, *inv = (uint32_t *)(ws + ra), *sid = (uint32_t *)(ws + 2 * ra);
+  char *sw = ws + 3 * ra;
+  const int E = w->experts, mt = sort_max_tiles(rows, E);
+  uint32_t *off = (uint32_t *)sw;
+  uint32_t *te = (uint32_t *)(sw + align_up(((size_t)E + 2) * 4));
+  uint32_t *tr = (uint32_t *)((char *)te + align_up((size_t)mt * 4));
+  uint32_t *tc = (uint32_t *)((char *)tr + align_up((size_t)mt * 4));
+  hipError_t e = launch_sort(ids, rows, E, so, inv, sid, off, te, tr, tc, s);
+  if (e != hipSuccess) return hip_fail(kGatherOp, e);
+  GemmArgs g{};
+  g.A = x;
+  g.lda = w->in_features;
+  g.a_rows = so;
+  g.a_div = 1;
+  g.a_rows2 = x_rows;
+  g.K = w->in_features;
+  g.N = w->out_features;
+  set_weights(g, *w, nullptr, 0);
+  g.tile_expert = te;
+  g.tile_row0 = tr;
+  g.tile_count = tc;
+  g.expert_offsets = off;
+  g.max_tiles = mt;
+  g.C = out;
+  g.ldc = w->out_features;
+  g.c_rows = so;
+  e = launch_grouped_gemm(g, kEpiPlain, s);
+  return e == hipSuccess ? ok() : hip_fail(kGatherOp, e);
+}
+
+int astro_moe_quantized_matmul(const uint16_t *x, int32_t rows, const astro_moe_affine *w,
+                               uint16_t *out, void *stream) {
+  int rc = check_affine(kQmmOp, w, -1);
+  if (rc) return rc;
+  if (w->experts != 1) return fail(ASTRO_MOE_INVALID_ARGUMENT, kQmmOp, "a plain quantized matmul takes one weight matrix");
+  if (rows < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kQmmOp, "activation and weight arrays must both have rank at least two");
+  if (rows == 0) return ok();
+  if (!x || !out) return fail(ASTRO_MOE_INVALID_ARGUMENT, kQmmOp, "quantized matmul buffers must be non-null");
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if (w->out_features < 16) {
+    e = launch_qgemv_rows(x, rows, w->in_features, w->w, w->scales, w->biases, w->out_features,
+                          w->bits, w->group_size, out, s);
+  } else {
+    GemmArgs g{};
+    g.A = x;
+    g.lda = w->in_features;
+    g.a_div = 1;
+    g.K = w->in_features;
+    g.N = w->out_features;
+    g.M = rows;
+    set_weights(g, *w, nullptr, 0);
+    g.C = out;
+    g.ldc = w->out_features;
+    e = launch_grouped_gemm(g, kEpiPlain, s);
+  }
+  return e == hipSuccess ? ok() : hip_fail(kQmmOp, e);
+}
+
+int astro_moe_swiglu(const uint16_t *gate, const uint16_t *up, int64_t n, uint16_t *out,
+                     void *stream) {
+  if (n < 0 || (n > 0 && (!gate || !up || !out)))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, "apply a compiled MLX SwiGLU graph", "SwiGLU buffers must be non-null");
+  hipError_t e = launch_swiglu(gate, up, n, out, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail("apply a compiled MLX SwiGLU graph", e);
+}
+
+int astro_moe_sorted_weighted_sum(const uint16_t *sorted_outputs, const uint32_t *inverse_order,
+                                  const uint16_t *scores, int32_t tokens, int32_t top_k,
+                                  int32_t dim, uint16_t *out, void *stream) {
+  // sorted_expert_weighted_sum_inner (weighted_sum.rs:129-156)
+  if (tokens < 0 || top_k < 0 || dim <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kReduceOp,
+                "sorted expert outputs, inverse order, and scores have invalid shapes or dtypes");
+  if (tokens == 0) return ok();
+  if (!out || (top_k > 0 && (!sorted_outputs || !inverse_order || !scores)))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kReduceOp, "sorted expert outputs and inverse order must match selected scores");
+  hipError_t e = launch_combine(sorted_outputs, inverse_order, scores, tokens, top_k, dim, 1,
+                                nullptr, nullptr, nullptr, out, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(kReduceOp, e);
+}
+
+int astro_moe_unsorted_weighted_sum(const uint16_t *outputs, const uint16_t *scores,
+                                    int32_t tokens, int32_t top_k, int32_t dim, uint16_t *out,
+                                    void *stream) {
+  if (tokens < 0 || top_k < 0 || dim <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kReduceOp, "unsorted expert outputs and scores must include an assignment axis");
+  if (tokens == 0) return ok();
+  if (!out || (top_k > 0 && (!outputs || !scores)))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kReduceOp, "unsorted expert outputs and scores must be non-null");
+  hipError_t e = launch_combine(outputs, nullptr, scores, tokens, top_k, dim, 0, nullptr, nullptr,
+                                nullptr, out, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(kReduceOp, e);
+}
+
+int astro_moe_combine_shared(const uint16_t *sparse, const uint16_t *shared_out,
+                             const uint16_t *gate_logits, int32_t tokens, int32_t dim,
+                             uint16_t *out, void *stream) {
+  if (tokens < 0 || dim <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kCombineOp, "shared expert output must match the combined sparse-expert shape");
+  if (tokens == 0) return ok();
+  if (!sparse || !shared_out || !gate_logits || !out)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kCombineOp, "shared expert gate must provide one logit per token");
+  hipError_t e = launch_combine_shared(sparse, shared_out, gate_logits, tokens, dim, out, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(kCombineOp, e);
+}
+
+int astro_moe_shared_expert_workspace_bytes(const astro_moe_layer *layer, int32_t tokens,
+                                            size_t *bytes) {
+  if (!layer || tokens < 0 || !bytes || layer->shared_intermediate <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kCombineOp, "the layer has no shared expert");
+  *bytes = align_up((size_t)tokens * layer->shared_intermediate * 2);
+  return ok();
+}
+
+int astro_moe_shared_expert(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                            uint16_t *shared_out, uint16_t *gate_logits, void *workspace,
+                            size_t workspace_bytes, void *stream) {
+  int rc = check_layer(kCombineOp, layer);
+  if (rc) return rc;
+  if (layer->shared_intermediate <= 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kCombineOp, "the layer has no shared expert");
+  if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kCombineOp, "token count must not be negative");
+  if (tokens == 0) return ok();
+  const size_t need = align_up((size_t)tokens * layer->shared_intermediate * 2);
+  if (!workspace || workspace_bytes < need) return workspace_fail(kCombineOp, need, workspace ? workspace_bytes : 0);
+  if (!x || !shared_out || !gate_logits) return fail(ASTRO_MOE_INVALID_ARGUMENT, kCombineOp, "shared expert buffers must be non-null");
+  hipError_t e = run_shared(*layer, x, tokens, (uint16_t *)workspace, shared_out, gate_logits,
+                            (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(kCombineOp, e);
+}
+
+}  // extern "C"

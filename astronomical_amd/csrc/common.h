@@ -1,0 +1,101 @@
+// Device helpers shared by the gfx950 kernels: bf16 bit conversions, the
+// deterministic exp used by softmax/sigmoid, wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace astro {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+// IEEE round-to-nearest-even fp32 -> bf16 on the bit pattern (NaN stays quiet NaN).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return f2bf(lo) | (f2bf(hi) << 16);
+}
+
+// exp(x): Cody-Waite reduction x = n ln2 + r (|r| <= ln2/2), degree-7 Taylor polynomial
+// with explicit fma, exact power-of-two scale; e^x below e^-80 is 0 so no subnormal is
+// produced.  Only IEEE mul/fma/rint are used, so the host restatement of the same
+// steps returns identical bits.
+__device__ __forceinline__ float det_expf(float x) {
+#pragma clang fp contract(off)
+  if (x != x) return x;
+  if (x > 88.72283172607421875f) return __builtin_inff();
+  if (x < -80.0f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860676533018704e-6f, r);
+  float p = (float)(1.0 / 5040.0);
+  p = __builtin_fmaf(p, r, (float)(1.0 / 720.0));
+  p = __builtin_fmaf(p, r, (float)(1.0 / 120.0));
+  p = __builtin_fmaf(p, r, (float)(1.0 / 24.0));
+  p = __builtin_fmaf(p, r, (float)(1.0 / 6.0));
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  if (ni > 127) {
+    p = p * 2.0f;
+    ni -= 1;
+  }
+  return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+}
+
+__device__ __forceinline__ float det_sigmoid(float v) {
+#pragma clang fp contract(off)
+  return 1.0f / (1.0f + det_expf(-v));
+}
+
+// SwiGLU with the reference's three bf16 roundings (mlx_compiled_swiglu.rs:66-86):
+// s = bf16(sigmoid(g)); a = bf16(g*s); out = bf16(a*u).
+__device__ __forceinline__ uint32_t swiglu_bf(float g, float u) {
+#pragma clang fp contract(off)
+  const float s = round_bf(det_sigmoid(g));
+  const float a = round_bf(g * s);
+  return f2bf(a * u);
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.  The butterfly adds
+// lane j and lane j^off for off = 32, 16, ..., 1, i.e. the binary tree
+// lane[j] += lane[j + off] evaluated at lane 0.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma clang fp contract(off)
+  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+}  // namespace astro

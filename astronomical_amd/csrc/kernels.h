@@ -1,0 +1,83 @@
+// Internal launch interface of the gfx950 kernels (host side of each .hip file).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace astro {
+
+// Rows of one grouped-GEMM tile; also the row granularity of the tile table the sort
+// kernels emit.
+constexpr int kGemmBM = 128;
+
+enum BKind { kBQ4 = 0, kBQ8 = 1, kBDense = 2 };
+enum Epilogue { kEpiPlain = 0, kEpiSwiglu = 1, kEpiBias = 2 };
+
+// out[dst(r)][n] = epilogue( sum_k A[src(r)][k] * B[expert(r)][n][k] ) over the rows r of
+// every tile.  Tiles come from the tile table (expert, first row) written by the sort,
+// or, when tile_expert == nullptr, from one implicit group of M rows.
+struct GemmArgs {
+  const uint16_t *A;
+  int64_t lda;
+  const uint32_t *a_rows;  // sorted row -> source index (nullptr: identity)
+  int a_div;               // source row = a_rows[r] / a_div
+  const uint32_t *a_rows2; // optional second indirection: source row = a_rows2[that]
+  int K;
+  int N;                   // output columns (activated columns for the SwiGLU epilogue)
+  int bkind;
+  // affine weights: gate (or the only projection) and, for SwiGLU, up
+  const uint32_t *w0, *w1;
+  const uint16_t *s0, *s1, *b0, *b1;
+  int64_t w_expert_stride, w_row_stride;    // in u32 words
+  int64_t sb_expert_stride, sb_row_stride;  // in bf16 elements
+  int group;
+  // dense bf16 weights [N][K]
+  const uint16_t *bd;
+  int64_t bd_row_stride;
+  const uint16_t *bias;    // kEpiBias: bf16 [N]
+  // tiles
+  const uint32_t *tile_expert;
+  const uint32_t *tile_row0;
+  const uint32_t *tile_count;
+  const uint32_t *expert_offsets;
+  int M;                   // rows of the implicit single group
+  int max_tiles;
+  // output
+  uint16_t *C;
+  int64_t ldc;
+  const uint32_t *c_rows;  // sorted row -> destination row (nullptr: identity)
+};
+
+hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s);
+
+hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
+                             uint32_t *idx, uint16_t *scores, hipStream_t s);
+
+// counting sort of assignment ids by expert (stable), plus the grouped-GEMM tile table
+// (tiles of kGemmBM rows).  offsets has E+2 entries (ids >= E land in a trailing
+// bucket that no tile covers).
+hipError_t launch_sort(const uint32_t *ids, int A, int E, uint32_t *sorted_order,
+                       uint32_t *inverse_order, uint32_t *sorted_ids, uint32_t *offsets,
+                       uint32_t *tile_expert, uint32_t *tile_row0, uint32_t *tile_count,
+                       hipStream_t s);
+int sort_max_tiles(int A, int E);
+
+// out[t] = bf16( x[t] . deq(W row n) ) for a few output rows (wave per (token, row)).
+hipError_t launch_qgemv_rows(const uint16_t *x, int T, int K, const uint32_t *w,
+                             const uint16_t *sc, const uint16_t *bi, int N, int bits, int group,
+                             uint16_t *out, hipStream_t s);
+
+hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *out,
+                         hipStream_t s);
+// y = weighted sum of expert rows (rows located through inverse_order), sorted (fp32
+// fma accumulation) or unsorted (bf16 products) rounding, then optionally the shared
+// expert's gated add.
+hipError_t launch_combine(const uint16_t *rows, const uint32_t *inverse_order,
+                          const uint16_t *scores, int T, int k, int D, int sorted,
+                          const uint16_t *shared_out, const uint16_t *gate_logits,
+                          uint16_t *sparse_out, uint16_t *y, hipStream_t s);
+hipError_t launch_combine_shared(const uint16_t *sparse, const uint16_t *shared_out,
+                                 const uint16_t *gate_logits, int T, int D, uint16_t *y,
+                                 hipStream_t s);
+
+}  // namespace astro

@@ -1,0 +1,375 @@
+"""Host-side mirror of the reference's MoE operator API over the C ABI.
+
+Function names, argument meaning and error behaviour follow the reference
+(crates/model-serving/src/sparse_experts/*.rs, qwen3_5_moe/model/{routing,output_combination}.rs,
+crates/runtime-integration/src/mlx_quantized_operations.rs).  Tensors are torch device
+tensors used as plain HBM buffers: bf16 as ``torch.bfloat16``, uint32 indices and packed
+codes as ``torch.int32`` bit patterns.  Every computation runs in libastro_moe.so on the
+tensors' current HIP stream; errors raise ``AstroMoeError`` with the library's message.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from enum import Enum
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import AstroMoeError, Affine, Layer, WorkspaceView, call
+from .layout import AffineWeights, MoeLayerWeights
+
+MINIMUM_SORTED_EXPERT_ASSIGNMENTS = 64  # routing.rs:13
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(device=None):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _bf16_dev(a, device="cuda") -> torch.Tensor:
+    if isinstance(a, torch.Tensor):
+        return a.to(device).contiguous().view(torch.bfloat16)
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).to(device).view(torch.bfloat16)
+
+
+def _u32_dev(a, device="cuda") -> torch.Tensor:
+    if isinstance(a, torch.Tensor):
+        return a.to(device).contiguous().view(torch.int32)
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(device)
+
+
+def to_device(L: MoeLayerWeights, device="cuda") -> MoeLayerWeights:
+    """Copy a host (numpy) layer to device tensors."""
+    def conv(a):
+        a = np.asarray(a)
+        return _u32_dev(a, device) if a.dtype == np.uint32 else _bf16_dev(a, device)
+    return L.map(conv)
+
+
+def bf16_to_numpy(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def u32_to_numpy(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.int32).cpu().numpy().view(np.uint32)
+
+
+def affine_struct(w: Optional[AffineWeights]) -> Affine:
+    if w is None:
+        return Affine()
+    return Affine(w.w.data_ptr(), w.scales.data_ptr(), w.biases.data_ptr(), int(w.w.shape[0]),
+                  int(w.w.shape[1]), int(w.w.shape[2]) * 32 // w.bits, w.bits, w.group_size)
+
+
+def layer_struct(L: MoeLayerWeights) -> Layer:
+    s = Layer()
+    s.hidden, s.num_experts, s.top_k = L.hidden, L.num_experts, L.top_k
+    s.intermediate, s.shared_intermediate = L.intermediate, L.shared_intermediate
+    s.normalize_top_k = int(bool(L.normalize_top_k))
+    s.router_w = None if L.router_w is None else L.router_w.data_ptr()
+    s.router_q = affine_struct(L.router_q)
+    s.router_bias = None if L.router_bias is None else L.router_bias.data_ptr()
+    s.gate_up = affine_struct(L.gate_up)
+    s.gate = affine_struct(L.gate)
+    s.up = affine_struct(L.up)
+    s.down = affine_struct(L.down)
+    s.shared_gate = affine_struct(L.shared_gate)
+    s.shared_up = affine_struct(L.shared_up)
+    s.shared_down = affine_struct(L.shared_down)
+    s.shared_expert_gate = affine_struct(L.shared_expert_gate)
+    return s
+
+
+# ---------------------------------------------------------------- routing (routing.rs)
+
+def qwen3_5_moe_route_experts(router_logits: torch.Tensor, expert_count_per_token: int,
+                              should_normalize_scores: bool):
+    """routing.rs:16-48 -> (selected_indices int32[..., k], selected_scores bf16[..., k])."""
+    if router_logits.dim() < 2:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "route Qwen3.5-MoE sparse experts: router "
+                            "logits must include token and expert dimensions")
+    if router_logits.dtype != torch.bfloat16:
+        raise AstroMoeError(_lib.UNSUPPORTED, "route Qwen3.5-MoE sparse experts: the kernels "
+                            "take bfloat16 router logits")
+    E = router_logits.shape[-1]
+    lg = router_logits.contiguous()
+    T = lg.numel() // max(E, 1)
+    k = int(expert_count_per_token)
+    shape = list(lg.shape[:-1]) + [max(k, 0)]
+    idx = torch.empty(shape, dtype=torch.int32, device=lg.device)
+    sc = torch.empty(shape, dtype=torch.bfloat16, device=lg.device)
+    call("astro_moe_route_topk", _ptr(lg), T, E, k, int(bool(should_normalize_scores)), _ptr(idx),
+         _ptr(sc), _stream(lg.device))
+    return idx, sc
+
+
+# ------------------------------------------------- sorting (assignment_sort.rs, permutation)
+
+@dataclass
+class SortedExpertAssignments:
+    """assignment_sort.rs:13-17; the row gather (sorted_states) is fused into
+    gather_qmm through ``token_rows`` instead of being materialised."""
+    sorted_order: torch.Tensor     # sorted slot -> original slot
+    sorted_indices: torch.Tensor   # expert id per sorted slot
+    inverse_order: torch.Tensor    # original slot -> sorted slot
+    expert_offsets: torch.Tensor   # [E+1]
+    expert_count_per_token: int
+
+    @property
+    def token_rows(self) -> torch.Tensor:
+        return torch.div(self.sorted_order, self.expert_count_per_token, rounding_mode="floor")
+
+
+def sort_expert_assignments(selected_indices: torch.Tensor, num_experts: int) -> SortedExpertAssignments:
+    """assignment_sort.rs:36-97: stable argsort by expert id, its inverse and the sorted ids."""
+    ids = selected_indices.contiguous().view(torch.int32)
+    if ids.dim() < 1:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "sort stacked expert assignments: selected "
+                            "expert indices must include an expert dimension")
+    k = int(ids.shape[-1]) if ids.dim() >= 2 else 1
+    A = ids.numel()
+    dev = ids.device
+    so = torch.empty(A, dtype=torch.int32, device=dev)
+    inv = torch.empty(A, dtype=torch.int32, device=dev)
+    sid = torch.empty(A, dtype=torch.int32, device=dev)
+    off = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    need = C.c_size_t()
+    call("astro_moe_sort_workspace_bytes", A, num_experts, C.byref(need))
+    ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=dev)
+    call("astro_moe_sort_assignments", _ptr(ids), A, num_experts, _ptr(so), _ptr(inv), _ptr(sid),
+         _ptr(off), _ptr(ws), need.value, _stream(dev))
+    return SortedExpertAssignments(so, sid, inv, off, k)
+
+
+def invert_assignment_order(sorted_order: Sequence[int]) -> list:
+    """assignment_permutation.rs:10-42 (host)."""
+    a = np.ascontiguousarray(np.asarray(sorted_order, dtype=np.uint32))
+    out = np.empty_like(a)
+    call("astro_moe_invert_assignment_order", C.c_void_p(a.ctypes.data), a.shape[0],
+         C.c_void_p(out.ctypes.data))
+    return out.tolist()
+
+
+def gathered_indices_use_sorted_contract(assignments_were_sorted: bool) -> bool:
+    """assignment_permutation.rs:44-48."""
+    return bool(assignments_were_sorted)
+
+
+# ------------------------------------------------- gathered projection (gathered_projection.rs)
+
+class ExpertAssignmentOrder(Enum):
+    ORIGINAL = 0
+    SORTED_BY_EXPERT = 1
+
+    def uses_sorted_indices(self) -> bool:
+        return self is ExpertAssignmentOrder.SORTED_BY_EXPERT
+
+
+def gather_expert_projection(activations: torch.Tensor, projection: AffineWeights,
+                             selected_expert_indices: torch.Tensor,
+                             assignment_order: ExpertAssignmentOrder = ExpertAssignmentOrder.ORIGINAL,
+                             token_rows: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gathered_projection.rs:84-131: out[r] = x[token_rows[r] or r] . deq(W[ids[r]])^T."""
+    x = activations.contiguous().view(torch.bfloat16)
+    ids = selected_expert_indices.contiguous().view(torch.int32).reshape(-1)
+    rows = ids.numel()
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    tr = None if token_rows is None else token_rows.contiguous().view(torch.int32).reshape(-1)
+    w = affine_struct(projection)
+    out = torch.empty(rows, w.out_features, dtype=torch.bfloat16, device=x.device)
+    if K != w.in_features:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "build affine gather_qmm: activation inner "
+                            "dimension does not match the expanded quantized weight input")
+    if tr is None and x2.shape[0] != rows:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "build affine gather_qmm: activation rows "
+                            "must match the assignment count when no token rows are given")
+    need = C.c_size_t()
+    call("astro_moe_gather_qmm_workspace_bytes", rows, w.experts, C.byref(need))
+    ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x.device)
+    call("astro_moe_gather_qmm", _ptr(x2), _ptr(tr), rows, C.byref(w), _ptr(ids),
+         int(assignment_order.uses_sorted_indices()), _ptr(out), _ptr(ws), need.value,
+         _stream(x.device))
+    return out
+
+
+def quantized_matmul_affine(activations: torch.Tensor, weights: AffineWeights) -> torch.Tensor:
+    """mlx_quantized_operations.rs:49-96 (transpose = true)."""
+    x = activations.contiguous().view(torch.bfloat16)
+    w = affine_struct(weights)
+    if x.shape[-1] != w.in_features:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "build affine quantized matmul: activation "
+                            "inner dimension does not match the expanded quantized weight input")
+    x2 = x.reshape(-1, x.shape[-1])
+    out = torch.empty(x2.shape[0], w.out_features, dtype=torch.bfloat16, device=x.device)
+    call("astro_moe_quantized_matmul", _ptr(x2), x2.shape[0], C.byref(w), _ptr(out), _stream(x.device))
+    return out.reshape(*x.shape[:-1], w.out_features)
+
+
+def apply_compiled_swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """mlx_compiled_swiglu.rs:44-89: silu(gate) * up in bf16."""
+    g, u = gate.contiguous(), up.contiguous()
+    if g.shape != u.shape:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "apply a compiled MLX SwiGLU graph: gate and "
+                            "input shapes must match")
+    out = torch.empty_like(g)
+    call("astro_moe_swiglu", _ptr(g), _ptr(u), g.numel(), _ptr(out), _stream(g.device))
+    return out
+
+
+# ------------------------------------------------- reductions (weighted_sum.rs)
+
+def sorted_expert_weighted_sum(sorted_expert_outputs: torch.Tensor, inverse_order: torch.Tensor,
+                               selected_scores: torch.Tensor) -> torch.Tensor:
+    """weighted_sum.rs:122-192: outputs [A, 1, D] (or [A, D]) in sorted order."""
+    so = sorted_expert_outputs.contiguous()
+    sc = selected_scores.contiguous()
+    if sc.dtype != torch.bfloat16 or so.dtype != torch.bfloat16:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "reduce stacked expert outputs: sorted expert "
+                            "outputs, inverse order, and scores have invalid shapes or dtypes")
+    k = sc.shape[-1]
+    A = sc.numel()
+    T = A // k if k else (sc.numel())
+    D = so.shape[-1]
+    if so.numel() // max(D, 1) != A or inverse_order.numel() != A:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "reduce stacked expert outputs: sorted expert "
+                            "outputs and inverse order must match selected scores")
+    out = torch.empty(*sc.shape[:-1], D, dtype=so.dtype, device=so.device)
+    call("astro_moe_sorted_weighted_sum", _ptr(so), _ptr(inverse_order.contiguous().view(torch.int32)),
+         _ptr(sc), T, k, D, _ptr(out), _stream(so.device))
+    return out
+
+
+def unsorted_expert_weighted_sum(selected_expert_outputs: torch.Tensor,
+                                 selected_scores: torch.Tensor) -> torch.Tensor:
+    """weighted_sum.rs:94-120: outputs [..., k, D] * scores [..., k] summed over k."""
+    o = selected_expert_outputs.contiguous()
+    sc = selected_scores.contiguous()
+    k = sc.shape[-1]
+    D = o.shape[-1]
+    T = sc.numel() // k if k else int(np.prod(sc.shape[:-1]))
+    out = torch.empty(*sc.shape[:-1], D, dtype=o.dtype, device=o.device)
+    call("astro_moe_unsorted_weighted_sum", _ptr(o), _ptr(sc), T, k, D, _ptr(out), _stream(o.device))
+    return out
+
+
+def combine_sparse_and_shared_experts(sparse_expert_output: torch.Tensor,
+                                      shared_expert_output: torch.Tensor,
+                                      shared_expert_gate_logits: torch.Tensor) -> torch.Tensor:
+    """output_combination.rs:34-43: sparse + shared * sigmoid(gate)."""
+    sp, so = sparse_expert_output.contiguous(), shared_expert_output.contiguous()
+    z = shared_expert_gate_logits.contiguous()
+    D = sp.shape[-1]
+    T = sp.numel() // D
+    if so.shape != sp.shape:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "combine Qwen3.5-MoE sparse and shared experts: "
+                            "shared expert output must match the combined sparse-expert shape")
+    if z.numel() != T:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "combine Qwen3.5-MoE sparse and shared experts: "
+                            "shared expert gate must provide one logit per token")
+    out = torch.empty_like(sp)
+    call("astro_moe_combine_shared", _ptr(sp), _ptr(so), _ptr(z), T, D, _ptr(out), _stream(sp.device))
+    return out
+
+
+def qwen3_5_moe_combine_experts(selected_expert_outputs, selected_scores, shared_expert_output,
+                                shared_expert_gate_logits):
+    """output_combination.rs:7-32."""
+    sparse = unsorted_expert_weighted_sum(selected_expert_outputs, selected_scores)
+    return combine_sparse_and_shared_experts(sparse, shared_expert_output, shared_expert_gate_logits)
+
+
+# ------------------------------------------------- the whole block (forward.rs:19-127)
+
+class MoeBlock:
+    """One resident MoE block: borrowed device weights + a reusable workspace."""
+
+    def __init__(self, weights: MoeLayerWeights, device="cuda"):
+        self.weights = weights
+        self.device = torch.device(device)
+        self._struct = layer_struct(weights)
+        self._ws = None
+        self._ws_tokens = -1
+
+    def workspace_bytes(self, tokens: int) -> int:
+        n = C.c_size_t()
+        call("astro_moe_workspace_bytes", C.byref(self._struct), tokens, C.byref(n))
+        return n.value
+
+    def workspace(self, tokens: int) -> torch.Tensor:
+        need = self.workspace_bytes(tokens)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(max(need, 1), dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+        x2 = x.contiguous().view(torch.bfloat16).reshape(-1, self.weights.hidden)
+        T = x2.shape[0]
+        y = out if out is not None else torch.empty_like(x2)
+        ws = workspace if workspace is not None else self.workspace(T)
+        call("astro_moe_block_forward", C.byref(self._struct), _ptr(x2), T, _ptr(y), _ptr(ws),
+             ws.numel(), _stream(self.device))
+        return y
+
+    __call__ = forward
+
+    def trace(self, tokens: int, workspace: Optional[torch.Tensor] = None) -> dict:
+        """Intermediates of the last forward with `tokens` tokens (host numpy copies)."""
+        v = WorkspaceView()
+        call("astro_moe_workspace_layout", C.byref(self._struct), tokens, C.byref(v))
+        ws = workspace if workspace is not None else self._ws
+        torch.cuda.synchronize(self.device)
+        raw = ws[: v.total_bytes].cpu().numpy()
+        L = self.weights
+        T, E, k, H, I = tokens, L.num_experts, L.top_k, L.hidden, L.intermediate
+        A = T * k
+
+        def get(off, n, dt):
+            return raw[off: off + n * np.dtype(dt).itemsize].view(dt).copy()
+        out = dict(
+            sorted_path=bool(v.sorted_path),
+            logits=get(v.logits, T * E, np.uint16).reshape(T, E),
+            indices=get(v.indices, A, np.uint32).reshape(T, k),
+            scores=get(v.scores, A, np.uint16).reshape(T, k),
+            sorted_order=get(v.sorted_order, A, np.uint32),
+            inverse_order=get(v.inverse_order, A, np.uint32),
+            sorted_ids=get(v.sorted_ids, A, np.uint32),
+            expert_offsets=get(v.expert_offsets, E + 1, np.uint32),
+            activated_sorted=get(v.activated, A * I, np.uint16).reshape(A, I),
+            expert_out_sorted=get(v.expert_out, A * H, np.uint16).reshape(A, H),
+            sparse=get(v.sparse, T * H, np.uint16).reshape(T, H))
+        if L.shared_intermediate:
+            out["shared_out"] = get(v.shared_out, T * H, np.uint16).reshape(T, H)
+            out["shared_gate_logits"] = get(v.shared_gate_logits, T, np.uint16)
+        return out
+
+
+def router_logits(weights: MoeLayerWeights, x: torch.Tensor) -> torch.Tensor:
+    """forward.rs:52-93 (+ the optional logit bias)."""
+    s = layer_struct(weights)
+    x2 = x.contiguous().view(torch.bfloat16).reshape(-1, weights.hidden)
+    out = torch.empty(x2.shape[0], weights.num_experts, dtype=torch.bfloat16, device=x.device)
+    call("astro_moe_router_logits", C.byref(s), _ptr(x2), x2.shape[0], _ptr(out), _stream(x.device))
+    return out
+
+
+def shared_expert(weights: MoeLayerWeights, x: torch.Tensor):
+    """resident_execution.rs:360-382 -> (shared_out bf16 [T, H], gate_logits bf16 [T])."""
+    s = layer_struct(weights)
+    x2 = x.contiguous().view(torch.bfloat16).reshape(-1, weights.hidden)
+    T = x2.shape[0]
+    need = C.c_size_t()
+    call("astro_moe_shared_expert_workspace_bytes", C.byref(s), T, C.byref(need))
+    ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x.device)
+    so = torch.empty(T, weights.hidden, dtype=torch.bfloat16, device=x.device)
+    z = torch.empty(T, dtype=torch.bfloat16, device=x.device)
+    call("astro_moe_shared_expert", C.byref(s), _ptr(x2), T, _ptr(so), _ptr(z), _ptr(ws),
+         need.value, _stream(x.device))
+    return so, z

@@ -1,0 +1,215 @@
+/*
+ * astro_moe — MI355X (gfx950) sorted mixture-of-experts block behind a plain C ABI.
+ *
+ * This is the drop-in seam for the reference's MoE block.  The reference reaches the
+ * block through Qwen3_5Model::forward_qwen3_5_moe
+ * (crates/model-serving/src/qwen3_5_moe/model/forward.rs:19-28) and every operation
+ * below it through the MLX-C C ABI bound in crates/runtime-integration/src/raw.rs:1-11.
+ * Each entry point below names the reference function it replaces.
+ *
+ * Conventions (mirroring MLX-C, crates/runtime-integration/src/mlx_runtime/error_handling.rs:19-62):
+ *  - every call returns an int status, 0 = success;
+ *  - on failure astro_moe_last_error() returns a thread-local message of the form
+ *    "<operation>: <description>"; a too-small workspace carries the marker
+ *    "ASTRONOMICAL_MLX_ACTIVE_MEMORY_LIMIT_EXCEEDED active_bytes=0 allocation_bytes=<needed>
+ *    allowed_bytes=<given>" so classify_mlx_error (error_handling.rs:57-62, :81-122) still
+ *    returns ActiveMemoryLimitExceeded;
+ *  - bf16 tensors are uint16_t bit patterns; packed affine weights are uint32_t in MLX
+ *    layout (element j of a row = bits [j*b, j*b+b) of the row's little-endian bit
+ *    stream); scales/biases are bf16;
+ *  - all pointers are device pointers (HBM) unless stated; the caller owns every buffer
+ *    and the library never allocates on the hot path — scratch comes from `workspace`;
+ *  - `stream` is a hipStream_t (NULL = the default stream); every launch is
+ *    asynchronous on it; no global mutable state besides the thread-local error.
+ *  - No C++ exception crosses this ABI.
+ */
+#ifndef ASTRO_MOE_H
+#define ASTRO_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ASTRO_MOE_ABI_VERSION 1
+
+enum astro_moe_status {
+  ASTRO_MOE_OK = 0,
+  ASTRO_MOE_INVALID_ARGUMENT = 1,      /* geometry, dtype contract or null pointer */
+  ASTRO_MOE_UNSUPPORTED = 2,           /* valid for MLX, not implemented by the kernels */
+  ASTRO_MOE_WORKSPACE_TOO_SMALL = 3,   /* message carries the active-memory marker */
+  ASTRO_MOE_HIP_ERROR = 4,             /* a HIP runtime call failed */
+};
+
+/*
+ * One stacked affine projection in MLX layout (gathered_projection.rs:50-71,
+ * StackedExpertProjection::Affine): w [experts][out][in*bits/32] u32,
+ * scales/biases [experts][out][in/group] bf16.  experts == 1 for a plain quantized
+ * linear (router, shared expert).  Kernels implement bits in {4, 8} and group in
+ * {32, 64, 128}; other MLX widths return ASTRO_MOE_UNSUPPORTED.
+ */
+typedef struct astro_moe_affine {
+  const uint32_t *w;
+  const uint16_t *scales;
+  const uint16_t *biases;
+  int32_t experts;
+  int32_t out_features;
+  int32_t in_features;
+  int32_t bits;
+  int32_t group_size;
+} astro_moe_affine;
+
+/*
+ * Borrowed weights of one block (Qwen3_5MoEFeedForwardWeights, feed_forward_weights.rs:17-24,
+ * and the resident expert arrays, resident_expert_layer_weights.rs:12-16).  Exactly one
+ * of router_w / router_q.w is set.  gate_up.w set selects the fused resident layout
+ * [E][2I][H*b/32] (resident_gate_up_fusion.rs:221-260); otherwise gate and up are
+ * separate pages.  shared_intermediate == 0 means no shared expert.
+ */
+typedef struct astro_moe_layer {
+  int32_t hidden;              /* H */
+  int32_t num_experts;         /* E */
+  int32_t top_k;               /* k */
+  int32_t intermediate;        /* I */
+  int32_t shared_intermediate; /* Is */
+  int32_t normalize_top_k;     /* norm_topk_prob (config_document.rs:145) */
+  const uint16_t *router_w;    /* bf16 [E][H] (unquantized router, forward.rs:59-91) */
+  astro_moe_affine router_q;   /* affine router (forward.rs:53-58) */
+  const uint16_t *router_bias; /* optional bf16 [E] added to the logits (benchmark skew only) */
+  astro_moe_affine gate_up;
+  astro_moe_affine gate;
+  astro_moe_affine up;
+  astro_moe_affine down;                /* [E][H][I*b/32] */
+  astro_moe_affine shared_gate;         /* [1][Is][H*b/32] */
+  astro_moe_affine shared_up;
+  astro_moe_affine shared_down;         /* [1][H][Is*b/32] */
+  astro_moe_affine shared_expert_gate;  /* [1][1][H*b/32] */
+  const uint32_t *slot_of_expert; /* reserved for compact paged pages; must be NULL */
+} astro_moe_layer;
+
+/* Byte offsets of the block's intermediates inside the workspace, valid after
+ * astro_moe_block_forward with the same layer and token count (for inspection and
+ * tests; the hot path never reads this). Offsets are from the workspace base. */
+typedef struct astro_moe_workspace_view {
+  size_t total_bytes;
+  int32_t sorted_path;       /* 1 when T*k >= 64 (routing.rs:13) */
+  size_t logits;             /* bf16 [T][E] */
+  size_t indices;            /* u32 [T][k] */
+  size_t scores;             /* bf16 [T][k] */
+  size_t sorted_order;       /* u32 [A]: sorted slot -> original slot */
+  size_t inverse_order;      /* u32 [A]: original slot -> sorted slot */
+  size_t sorted_ids;         /* u32 [A] */
+  size_t expert_offsets;     /* u32 [E+1] */
+  size_t activated;          /* bf16 [A][I], sorted order */
+  size_t expert_out;         /* bf16 [A][H], sorted order */
+  size_t sparse;             /* bf16 [T][H] */
+  size_t shared_out;         /* bf16 [T][H] */
+  size_t shared_gate_logits; /* bf16 [T] */
+} astro_moe_workspace_view;
+
+const char *astro_moe_last_error(void);
+int astro_moe_abi_version(void);
+
+/* Workspace sizing for astro_moe_block_forward (host-only, no GPU call). */
+int astro_moe_workspace_bytes(const astro_moe_layer *layer, int32_t tokens, size_t *bytes);
+int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
+                               astro_moe_workspace_view *view);
+
+/*
+ * Whole block, y = MoE(x): replaces Qwen3_5Model::forward_qwen3_5_moe with the
+ * resident owner (forward.rs:19-127 -> resident_execution.rs:70-143, :352-400).
+ * x, y: bf16 [tokens][H].  The residual add stays with the caller
+ * (decoder_layer_forward.rs:172-173).
+ */
+int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                            uint16_t *y, void *workspace, size_t workspace_bytes,
+                            void *stream);
+
+/* Router projection logits = x·W_rᵀ (bf16 out, fp32 accumulate), plus router_bias if
+ * set: forward.rs:52-93 (matmul or quantized_linear). */
+int astro_moe_router_logits(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                            uint16_t *logits, void *stream);
+
+/* qwen3_5_moe_route_experts (routing.rs:16-48): softmax, top-k, optional
+ * renormalisation.  indices u32 [T][k] (ascending in (probability, index)),
+ * scores bf16 [T][k]. */
+int astro_moe_route_topk(const uint16_t *logits, int32_t tokens, int32_t experts,
+                         int32_t top_k, int32_t normalize, uint32_t *indices,
+                         uint16_t *scores, void *stream);
+
+/* sort_expert_assignments (assignment_sort.rs:36-97) minus the row gather, which the
+ * gathered matmul fuses into its activation load: sorted_order = stable argsort(ids),
+ * inverse_order, sorted_ids, expert_offsets [E+1]. */
+int astro_moe_sort_workspace_bytes(int32_t assignments, int32_t experts, size_t *bytes);
+int astro_moe_sort_assignments(const uint32_t *ids, int32_t assignments, int32_t experts,
+                               uint32_t *sorted_order, uint32_t *inverse_order,
+                               uint32_t *sorted_ids, uint32_t *expert_offsets,
+                               void *workspace, size_t workspace_bytes, void *stream);
+
+/* invert_assignment_order (assignment_permutation.rs:10-42); HOST pointers, no GPU. */
+int astro_moe_invert_assignment_order(const uint32_t *sorted_order, int32_t n,
+                                      uint32_t *inverse_order);
+
+/*
+ * gather_expert_projection / MlxRuntime::gather_quantized_matmul_affine
+ * (gathered_projection.rs:84-131, mlx_quantized_operations.rs:100-157, transpose = true):
+ * out[r] = x[x_rows ? x_rows[r] : r] · deq(W[ids[r]])ᵀ, bf16 [rows][out_features].
+ * sorted_indices is the caller's promise that ids ascend (gathered_projection.rs:18-43);
+ * results do not depend on it.
+ */
+int astro_moe_gather_qmm_workspace_bytes(int32_t rows, int32_t experts, size_t *bytes);
+int astro_moe_gather_qmm(const uint16_t *x, const uint32_t *x_rows, int32_t rows,
+                         const astro_moe_affine *w, const uint32_t *ids,
+                         int32_t sorted_indices, uint16_t *out, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
+/* quantized_matmul_affine (mlx_quantized_operations.rs:49-96) for w.experts == 1. */
+int astro_moe_quantized_matmul(const uint16_t *x, int32_t rows, const astro_moe_affine *w,
+                               uint16_t *out, void *stream);
+
+/* apply_compiled_swiglu (mlx_compiled_swiglu.rs:44-89): silu(gate) * up, bf16. */
+int astro_moe_swiglu(const uint16_t *gate, const uint16_t *up, int64_t n, uint16_t *out,
+                     void *stream);
+
+/* sorted_expert_weighted_sum (weighted_sum.rs:16-33, :122-192). */
+int astro_moe_sorted_weighted_sum(const uint16_t *sorted_outputs, const uint32_t *inverse_order,
+                                  const uint16_t *scores, int32_t tokens, int32_t top_k,
+                                  int32_t dim, uint16_t *out, void *stream);
+
+/* unsorted_expert_weighted_sum (weighted_sum.rs:94-120): outputs [T][k][D]. */
+int astro_moe_unsorted_weighted_sum(const uint16_t *outputs, const uint16_t *scores,
+                                    int32_t tokens, int32_t top_k, int32_t dim,
+                                    uint16_t *out, void *stream);
+
+/* combine_sparse_and_shared_experts (output_combination.rs:34-43). */
+int astro_moe_combine_shared(const uint16_t *sparse, const uint16_t *shared_out,
+                             const uint16_t *gate_logits, int32_t tokens, int32_t dim,
+                             uint16_t *out, void *stream);
+
+/* Shared expert of combine_resident_sparse_and_shared_experts (resident_execution.rs:360-382):
+ * shared_out = down(swiglu(gate(x), up(x))), gate_logits = shared_expert_gate(x). */
+int astro_moe_shared_expert_workspace_bytes(const astro_moe_layer *layer, int32_t tokens,
+                                            size_t *bytes);
+int astro_moe_shared_expert(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                            uint16_t *shared_out, uint16_t *gate_logits, void *workspace,
+                            size_t workspace_bytes, void *stream);
+
+/*
+ * Seeded synthetic inputs for benchmarks and tests (no counterpart in the reference):
+ * device-side version of astronomical_amd/synthetic.py.  key = stream key of the tensor.
+ */
+int astro_synth_words(uint32_t *out, int64_t n, uint64_t key, void *stream);
+int astro_synth_uniform_bf16(uint16_t *out, int64_t n, uint64_t key, double lo, double hi,
+                             void *stream);
+int astro_synth_affine_biases(uint16_t *out, const uint16_t *scales, int64_t n, uint64_t key,
+                              double center, double noise, void *stream);
+int astro_synth_normal_bf16(uint16_t *out, int64_t n, uint64_t key, double scale, void *stream);
+int astro_synth_activations(uint16_t *out, int32_t tokens, int32_t hidden, uint64_t key,
+                            void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,309 @@
+"""HIP path vs the CPU oracle, through the C ABI, on an MI355X.
+
+Bars: integer and index outputs (routing ids, permutation, offsets) bit-exact; the
+deterministic elementwise stages (SwiGLU, weighted sums, shared combine) bit-exact;
+matmul outputs (bf16 out, fp32 accumulation; the MFMA path rounds dequantised weights
+to bf16) within rel-L2 1e-2 and a median of 2 bf16 ulps (moe_testutil)."""
+import os
+
+import numpy as np
+import pytest
+
+from astronomical_amd import configs as CF
+from astronomical_amd import synthetic as S
+from astronomical_amd.layout import AffineWeights, bf16_to_f32, f32_to_bf16, pack_codes
+
+from conftest import GOLDEN
+from moe_testutil import assert_bf16_close, ulp_distance
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    from astronomical_amd import ops as O
+    O._lib.lib()
+    return O
+
+
+def _dev_bf16(a):
+    from astronomical_amd.ops import _bf16_dev
+    return _bf16_dev(a)
+
+
+def _dev_u32(a):
+    from astronomical_amd.ops import _u32_dev
+    return _u32_dev(a)
+
+
+def _np(t):
+    from astronomical_amd.ops import bf16_to_numpy, u32_to_numpy
+    return bf16_to_numpy(t) if t.dtype == torch.bfloat16 else u32_to_numpy(t)
+
+
+# ------------------------------------------------------------------ routing
+
+@pytest.mark.parametrize("T,E,k", [(1, 256, 8), (8, 256, 8), (2048, 256, 8), (16, 32, 4),
+                                   (33, 128, 8), (5, 70, 3), (3, 1024, 64)])
+def test_route_topk_bit_exact(ops, orc, T, E, k):
+    rng = np.random.default_rng(T * 7 + E)
+    logits = f32_to_bf16((rng.standard_normal((T, E)) * 0.9).astype(np.float32))
+    logits[T // 2:] = f32_to_bf16(np.round(bf16_to_f32(logits[T // 2:]) * 4) / 4)  # many ties
+    want_idx, want_sc = orc.route_topk(logits, k, True)
+    idx, sc = ops.qwen3_5_moe_route_experts(_dev_bf16(logits), k, True)
+    assert np.array_equal(_np(idx), want_idx)
+    assert np.array_equal(_np(sc), want_sc)
+    want_idx2, want_sc2 = orc.route_topk(logits, k, False)
+    idx2, sc2 = ops.qwen3_5_moe_route_experts(_dev_bf16(logits), k, False)
+    assert np.array_equal(_np(idx2), want_idx2) and np.array_equal(_np(sc2), want_sc2)
+
+
+def test_route_ties_fixture(ops):
+    fx = np.load(os.path.join(GOLDEN, "route_ties.npz"), allow_pickle=False)
+    for E, k in ((256, 8), (32, 4)):
+        idx, _ = ops.qwen3_5_moe_route_experts(_dev_bf16(fx[f"logits_E{E}_k{k}"]), k, True)
+        assert np.array_equal(_np(idx), fx[f"indices_E{E}_k{k}"])
+
+
+def test_route_and_combine_kat(ops, kats):
+    d = kats["route_and_combine"]
+    idx, sc = ops.qwen3_5_moe_route_experts(_dev_bf16(f32_to_bf16(np.array([d["logits"]], np.float32))), 2, True)
+    assert _np(idx)[0].tolist() == [2, 3]
+    assert np.allclose(np.sort(bf16_to_f32(_np(sc)[0])), d["expected_sorted_scores"], rtol=2 ** -8)
+    eo = f32_to_bf16(np.array(d["expert_outputs"], np.float32))
+    selected = _dev_bf16(eo[_np(idx)[0].astype(np.int64)][None])
+    y = ops.qwen3_5_moe_combine_experts(selected, sc, _dev_bf16(f32_to_bf16(np.array([d["shared_output"]], np.float32))),
+                                        _dev_bf16(f32_to_bf16(np.array([d["shared_gate_logit"]], np.float32))))
+    assert np.allclose(bf16_to_f32(_np(y))[0], d["expected_combined"], rtol=2 ** -7)
+
+
+# ------------------------------------------------------------------ sort
+
+@pytest.mark.parametrize("A,E", [(6, 6), (64, 32), (16384, 256), (32768, 256), (4096, 128), (1, 4)])
+def test_sort_bit_exact(ops, orc, A, E):
+    rng = np.random.default_rng(A + E)
+    if A == 32768:  # skewed: most assignments on a few experts, many experts empty
+        ids = np.minimum(rng.zipf(1.3, size=A) - 1, E - 1).astype(np.uint32)
+    else:
+        ids = rng.integers(0, E, size=A).astype(np.uint32)
+    so, inv, sid, off = orc.sort_assignments(ids, E)
+    r = ops.sort_expert_assignments(_dev_u32(ids), E)
+    assert np.array_equal(_np(r.sorted_order), so)
+    assert np.array_equal(_np(r.inverse_order), inv)
+    assert np.array_equal(_np(r.sorted_indices), sid)
+    assert np.array_equal(_np(r.expert_offsets), off)
+
+
+def test_sort_kat(ops, kats):
+    d = kats["sort_and_restore"]
+    r = ops.sort_expert_assignments(_dev_u32(np.array(d["ids"], np.uint32).reshape(2, 3)), 6)
+    assert _np(r.sorted_indices).tolist() == d["expected_sorted_ids"]
+    assert _np(r.inverse_order).tolist() == d["expected_inverse"]
+    hidden = np.array(d["hidden"])
+    assert hidden[_np(r.sorted_order) // 3].tolist() == d["expected_sorted_states"]
+
+
+# ------------------------------------------------------------------ quantized matmuls
+
+def _aff_from_kat(d):
+    w = np.array(d["w"], np.uint32).reshape(d["w_shape"])
+    s = f32_to_bf16(np.array(d["scales"], np.float32)).reshape(d["sb_shape"])
+    b = f32_to_bf16(np.array(d["biases"], np.float32)).reshape(d["sb_shape"])
+    return AffineWeights(_dev_u32(w), _dev_bf16(s), _dev_bf16(b), d["bits"], d["group"])
+
+
+@pytest.mark.parametrize("name", ["qmm_4bit_g64", "qmm_8bit_g64"])
+def test_quantized_matmul_kats(ops, kats, name):
+    d = kats[name]
+    x = _dev_bf16(f32_to_bf16(np.array(d["x"], np.float32).reshape(d["x_shape"])))
+    y = ops.quantized_matmul_affine(x, _aff_from_kat(d))
+    assert bf16_to_f32(_np(y)).reshape(-1).tolist() == d["expected"]
+
+
+def test_gather_qmm_kat(ops, kats):
+    d = kats["gather_qmm_4bit"]
+    x = _dev_bf16(f32_to_bf16(np.array(d["x"], np.float32).reshape(d["x_shape"])))
+    y = ops.gather_expert_projection(x, _aff_from_kat(d), _dev_u32(np.array(d["ids"], np.uint32)),
+                                     token_rows=_dev_u32(np.zeros(2, np.uint32)))
+    assert bf16_to_f32(_np(y)).tolist() == d["expected"]
+
+
+def _random_affine(rng, E, N, K, bits, group):
+    codes = rng.integers(0, 1 << bits, size=(E, N, K))
+    w = pack_codes(codes, bits)
+    s = f32_to_bf16(rng.uniform(0.002, 0.02, size=(E, N, K // group)).astype(np.float32))
+    b = f32_to_bf16((-(1 << (bits - 1)) * bf16_to_f32(s) + rng.normal(0, 1e-3, s.shape)).astype(np.float32))
+    return AffineWeights(w, s, b, bits, group)
+
+
+@pytest.mark.parametrize("bits,group", [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)])
+@pytest.mark.parametrize("sorted_ids", [False, True])
+def test_gather_qmm_matches_oracle(ops, orc, bits, group, sorted_ids):
+    rng = np.random.default_rng(bits * 100 + group)
+    E, N, K, rows = 9, 192, 512, 300
+    aff = _random_affine(rng, E, N, K, bits, group)
+    x = f32_to_bf16(rng.standard_normal((rows, K)).astype(np.float32))
+    ids = rng.integers(0, E, size=rows).astype(np.uint32)
+    ids[:40] = 3  # one expert with more than one tile of rows
+    if sorted_ids:
+        ids = np.sort(ids)
+    want = orc.gather_qmm(x, aff, ids)
+    daff = aff.map(lambda a: _dev_u32(a) if a.dtype == np.uint32 else _dev_bf16(a))
+    order = ops.ExpertAssignmentOrder.SORTED_BY_EXPERT if sorted_ids else ops.ExpertAssignmentOrder.ORIGINAL
+    got = _np(ops.gather_expert_projection(_dev_bf16(x), daff, _dev_u32(ids), order))
+    assert_bf16_close(got, want, f"gather_qmm {bits}-bit g{group}")
+
+
+# ------------------------------------------------------------------ elementwise stages
+
+def test_swiglu_bit_exact(ops, orc):
+    rng = np.random.default_rng(2)
+    g = f32_to_bf16((rng.standard_normal(100003) * 4).astype(np.float32))
+    u = f32_to_bf16((rng.standard_normal(100003) * 4).astype(np.float32))
+    g[:6] = f32_to_bf16(np.array([0.0, -0.0, 90.0, -90.0, 1e-30, -200.0], np.float32))
+    assert np.array_equal(_np(ops.apply_compiled_swiglu(_dev_bf16(g), _dev_bf16(u))), orc.swiglu(g, u))
+
+
+def test_weighted_sums_bit_exact(ops, orc, kats):
+    rng = np.random.default_rng(4)
+    T, k, D = 37, 8, 2048
+    out = f32_to_bf16(rng.standard_normal((T * k, D)).astype(np.float32))
+    sc = f32_to_bf16(rng.dirichlet(np.ones(k), size=T).astype(np.float32))
+    perm = rng.permutation(T * k).astype(np.uint32)
+    sorted_out = np.empty_like(out)
+    sorted_out[perm] = out
+    got = ops.sorted_expert_weighted_sum(_dev_bf16(sorted_out), _dev_u32(perm), _dev_bf16(sc))
+    assert np.array_equal(_np(got), orc.sorted_weighted_sum(sorted_out, perm, sc))
+    got_u = ops.unsorted_expert_weighted_sum(_dev_bf16(out.reshape(T, k, D)), _dev_bf16(sc))
+    assert np.array_equal(_np(got_u), orc.unsorted_weighted_sum(out.reshape(T, k, D), sc))
+    d = kats["sorted_weighted_sum"]
+    y = ops.sorted_expert_weighted_sum(_dev_bf16(f32_to_bf16(np.array(d["sorted_outputs"], np.float32))),
+                                       _dev_u32(np.array(d["inverse"], np.uint32)),
+                                       _dev_bf16(f32_to_bf16(np.array(d["scores"], np.float32))))
+    assert np.allclose(bf16_to_f32(_np(y)), d["expected"], rtol=2 ** -7)
+    d = kats["unsorted_weighted_sum"]
+    y = ops.unsorted_expert_weighted_sum(_dev_bf16(f32_to_bf16(np.array(d["outputs"], np.float32))),
+                                         _dev_bf16(f32_to_bf16(np.array(d["scores"], np.float32))))
+    assert bf16_to_f32(_np(y)).tolist() == d["expected"]
+
+
+def test_combine_shared_bit_exact(ops, orc):
+    rng = np.random.default_rng(8)
+    T, D = 19, 1024
+    sp = f32_to_bf16(rng.standard_normal((T, D)).astype(np.float32))
+    so = f32_to_bf16(rng.standard_normal((T, D)).astype(np.float32))
+    z = f32_to_bf16(rng.standard_normal(T).astype(np.float32) * 3)
+    got = ops.combine_sparse_and_shared_experts(_dev_bf16(sp), _dev_bf16(so), _dev_bf16(z))
+    assert np.array_equal(_np(got), orc.combine_shared(sp, so, z))
+
+
+# ------------------------------------------------------------------ whole block
+
+def _device_layer(ops, L):
+    return ops.to_device(L)
+
+
+def _check_block(ops, orc, L, x, what):
+    """GPU block vs oracle: routing bit-exact on the GPU's logits, outputs to the FP bar."""
+    dL = _device_layer(ops, L)
+    blk = ops.MoeBlock(dL)
+    T = x.shape[0]
+    y = _np(blk(_dev_bf16(x)))
+    tr = blk.trace(T)
+    # router projection: fp32 accumulation in another order -> within one bf16 ulp
+    want_logits = orc.router_logits(x, L.router_w) if L.router_bias is None else None
+    if want_logits is not None:
+        u = ulp_distance(tr["logits"], want_logits)
+        assert u.max() <= 1, (what, int(u.max()))
+    # routing and permutation bit-exact given identical logits
+    y_ref, ref = orc.moe_block_forward(L, x, logits_override=tr["logits"], trace=True)
+    assert np.array_equal(tr["indices"], ref["indices"]), what
+    assert np.array_equal(tr["scores"], ref["scores"]), what
+    A = T * L.top_k
+    so, inv, sid, off = orc.sort_assignments(tr["indices"].reshape(-1), L.num_experts)
+    assert np.array_equal(tr["sorted_order"], so) and np.array_equal(tr["inverse_order"], inv)
+    assert np.array_equal(tr["sorted_ids"], sid) and np.array_equal(tr["expert_offsets"], off)
+    assert tr["sorted_path"] == (A >= 64) == ref["used_sorted_path"]
+    # intermediates and output
+    act = tr["activated_sorted"][inv]  # back to assignment order
+    stats = {"act": assert_bf16_close(act, ref["activated"], what + " activated")}
+    stats["expert_out"] = assert_bf16_close(tr["expert_out_sorted"][inv], ref["expert_out"], what + " expert_out")
+    stats["y"] = assert_bf16_close(y, y_ref, what + " y")
+    if L.shared_intermediate:
+        stats["shared"] = assert_bf16_close(tr["shared_out"], ref["shared_out"], what + " shared")
+    # end-to-end routing with the oracle's own router: tokens whose top-k set differs
+    _, ref2 = orc.moe_block_forward(L, x, trace=True)
+    differ = int(np.sum(np.any(np.sort(ref2["indices"], 1) != np.sort(tr["indices"], 1), axis=1)))
+    stats["tokens_with_different_topk_set"] = differ
+    assert differ <= max(1, T // 200), (what, differ)
+    print(what, stats)
+    return stats
+
+
+def test_block_c0_golden(ops, orc):
+    fx = np.load(os.path.join(GOLDEN, "c0_block.npz"), allow_pickle=False)
+    L = S.make_layer(CF.C0)
+    _check_block(ops, orc, L, fx["x"], "c0")
+    blk = ops.MoeBlock(_device_layer(ops, L))
+    y = _np(blk(_dev_bf16(fx["x"])))
+    assert_bf16_close(y, fx["y"], "c0 vs committed fixture")
+
+
+@pytest.fixture(scope="module")
+def c1_layer():
+    return S.make_layer(CF.C1)
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 8])
+def test_block_c1_decode(ops, orc, c1_layer, T):
+    _check_block(ops, orc, c1_layer, S.make_tokens(CF.C1, T), f"c1 B={T}")
+
+
+def test_block_c2_prefill_subset(ops, orc, c1_layer):
+    _check_block(ops, orc, c1_layer, S.make_tokens(CF.C2, 256), "c2 T=256")
+
+
+def test_block_c3_skewed_subset(ops, orc):
+    L = S.make_layer(CF.C3)
+    _check_block(ops, orc, L, S.make_tokens(CF.C3, 512), "c3 T=512 (Zipf)")
+
+
+def test_block_c4_8bit(ops, orc):
+    L = S.make_layer(CF.C4)
+    for T in (1, 64):
+        _check_block(ops, orc, L, S.make_tokens(CF.C4, T), f"c4 T={T}")
+
+
+def test_fused_and_separate_gate_up_are_bit_identical(ops):
+    """resident_gate_up_fusion.rs:13-90 on the device."""
+    L = S.make_layer(CF.C0, keep_separate=True)
+    x = _dev_bf16(S.make_tokens(CF.C0, 40))
+    fused = ops.MoeBlock(_device_layer(ops, L))
+    Ls = L.map(lambda a: a)
+    Ls.gate_up = None
+    sep = ops.MoeBlock(_device_layer(ops, Ls))
+    assert np.array_equal(_np(fused(x)), _np(sep(x)))
+
+
+def test_empty_token_batch(ops):
+    L = S.make_layer(CF.C0)
+    blk = ops.MoeBlock(_device_layer(ops, L))
+    y = blk(torch.empty(0, L.hidden, dtype=torch.bfloat16, device="cuda"))
+    assert y.shape == (0, L.hidden)
+
+
+def test_device_generator_matches_numpy(ops):
+    from astronomical_amd import device_synthetic as DS
+    cfg = CF.C0
+    host = S.make_layer(cfg)
+    dev = DS.make_layer_device(cfg)
+    assert np.array_equal(_np(dev.gate_up.w), host.gate_up.w)
+    assert np.array_equal(_np(dev.down.w), host.down.w)
+    for a, b in ((dev.gate_up.scales, host.gate_up.scales), (dev.gate_up.biases, host.gate_up.biases),
+                 (dev.router_w, host.router_w)):
+        assert np.mean(_np(a) == b) > 0.9999
+    xd = _np(DS.make_tokens_device(cfg, 16))
+    assert np.mean(xd == S.make_tokens(cfg, 16)) > 0.9999
