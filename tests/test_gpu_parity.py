@@ -216,8 +216,16 @@ def _check_block(ops, orc, L, x, what):
     # router projection: fp32 accumulation in another order -> within one bf16 ulp
     want_logits = orc.router_logits(x, L.router_w) if L.router_bias is None else None
     if want_logits is not None:
-        u = ulp_distance(tr["logits"], want_logits)
-        assert u.max() <= 1, (what, int(u.max()))
+        # two fp32 accumulation orders differ by a few 2^-24 * sum|x*w| (absolute), then
+        # each result is rounded to bf16: |diff| <= ulp(ref) + 2^-18 * sum|x*w|
+        xa = np.abs(bf16_to_f32(x).astype(np.float64))
+        wa = np.abs(bf16_to_f32(L.router_w).astype(np.float64))
+        mag = xa @ wa.T
+        ref = bf16_to_f32(want_logits).astype(np.float64)
+        got = bf16_to_f32(tr["logits"]).astype(np.float64)
+        ulp = np.abs(np.spacing(ref.astype(np.float32)).astype(np.float64)) * 2 ** 16
+        assert np.all(np.abs(got - ref) <= ulp + 2.0 ** -18 * mag), what
+        assert np.mean(ulp_distance(tr["logits"], want_logits) <= 1) > 0.999, what
     # routing and permutation bit-exact given identical logits
     y_ref, ref = orc.moe_block_forward(L, x, logits_override=tr["logits"], trace=True)
     assert np.array_equal(tr["indices"], ref["indices"]), what
