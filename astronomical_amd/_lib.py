@@ -12,6 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libastro_moe.so")
 
 OK, INVALID_ARGUMENT, UNSUPPORTED, WORKSPACE_TOO_SMALL, HIP_ERROR = 0, 1, 2, 3, 4
+STAGES = ("router", "route", "sort", "gate_up", "down", "shared", "combine")
 
 
 class AstroMoeError(RuntimeError):
@@ -54,6 +55,9 @@ EXPORTS = {
     "astro_moe_workspace_layout": ([C.POINTER(Layer), C.c_int32, C.POINTER(WorkspaceView)], C.c_int),
     "astro_moe_block_forward": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
                                  C.c_size_t, C.c_void_p], C.c_int),
+    "astro_moe_block_forward_attributed": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p,
+                                            C.c_void_p, C.c_size_t, C.c_void_p,
+                                            C.POINTER(C.c_float)], C.c_int),
     "astro_moe_router_logits": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
     "astro_moe_route_topk": ([C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                               C.c_void_p, C.c_void_p], C.c_int),

@@ -256,6 +256,109 @@ hipError_t run_shared(const astro_moe_layer &L, const uint16_t *x, int T, uint16
                            z, s);
 }
 
+// The block's launch sequence.  `marks` (nullable) receives ASTRO_MOE_STAGES + 1 event
+// records at the stage boundaries: router, route, sort, gate/up, down, shared, combine.
+int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, uint16_t *y,
+              void *workspace, size_t workspace_bytes, void *stream, hipEvent_t *marks) {
+  int rc = check_layer(kBlockOp, layer);
+  if (rc) return rc;
+  if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
+  if (tokens == 0) {
+    if (marks)
+      for (int i = 0; i <= ASTRO_MOE_STAGES; ++i) (void)hipEventRecord(marks[i], (hipStream_t)stream);
+    return ok();
+  }
+  if (!x || !y) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "hidden states and output must be non-null");
+  const astro_moe_layer &L = *layer;
+  const Layout o = block_layout(L, tokens);
+  if (!workspace || workspace_bytes < o.total) return workspace_fail(kBlockOp, o.total, workspace ? workspace_bytes : 0);
+  hipStream_t s = (hipStream_t)stream;
+  char *ws = (char *)workspace;
+  auto at = [&](size_t off) { return (void *)(ws + off); };
+  const int T = tokens, H = L.hidden, E = L.num_experts, k = L.top_k, I = L.intermediate;
+  const int A = T * k;
+  uint16_t *logits = (uint16_t *)at(o.logits);
+  uint32_t *idx = (uint32_t *)at(o.idx);
+  uint16_t *scores = (uint16_t *)at(o.scores);
+  uint32_t *sorted_order = (uint32_t *)at(o.sorted_order);
+  uint32_t *inverse = (uint32_t *)at(o.inverse);
+  uint32_t *sorted_ids = (uint32_t *)at(o.sorted_ids);
+  uint32_t *offsets = (uint32_t *)at(o.offsets);
+  uint32_t *tile_expert = (uint32_t *)at(o.tile_expert);
+  uint32_t *tile_row0 = (uint32_t *)at(o.tile_row0);
+  uint32_t *tile_count = (uint32_t *)at(o.tile_count);
+  uint16_t *act = (uint16_t *)at(o.act);
+  uint16_t *eout = (uint16_t *)at(o.eout);
+  uint16_t *sparse = (uint16_t *)at(o.sparse);
+
+  int stage = 0;
+  auto mark = [&]() {
+    if (marks) (void)hipEventRecord(marks[stage++], s);
+  };
+  mark();
+  hipError_t e = run_router(L, x, T, logits, s);
+  mark();
+  if (e == hipSuccess) e = launch_route_topk(logits, T, E, k, L.normalize_top_k, idx, scores, s);
+  mark();
+  if (e == hipSuccess)
+    e = launch_sort(idx, A, E, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
+                    tile_count, s);
+  mark();
+  if (e != hipSuccess) return hip_fail(kBlockOp, e);
+
+  // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / k]
+  GemmArgs gu{};
+  gu.A = x;
+  gu.lda = H;
+  gu.a_rows = sorted_order;
+  gu.a_div = k;
+  gu.K = H;
+  gu.N = I;
+  if (L.gate_up.w)
+    set_weights(gu, L.gate_up, &L.gate_up, I);
+  else
+    set_weights(gu, L.gate, &L.up, 0);
+  gu.tile_expert = tile_expert;
+  gu.tile_row0 = tile_row0;
+  gu.tile_count = tile_count;
+  gu.expert_offsets = offsets;
+  gu.max_tiles = o.max_tiles;
+  gu.C = act;
+  gu.ldc = I;
+  e = launch_grouped_gemm(gu, kEpiSwiglu, s);
+  mark();
+
+  GemmArgs dn{};
+  dn.A = act;
+  dn.lda = I;
+  dn.a_div = 1;
+  dn.K = I;
+  dn.N = H;
+  set_weights(dn, L.down, nullptr, 0);
+  dn.tile_expert = tile_expert;
+  dn.tile_row0 = tile_row0;
+  dn.tile_count = tile_count;
+  dn.expert_offsets = offsets;
+  dn.max_tiles = o.max_tiles;
+  dn.C = eout;
+  dn.ldc = H;
+  if (e == hipSuccess) e = launch_grouped_gemm(dn, kEpiPlain, s);
+  mark();
+
+  const bool has_shared = L.shared_intermediate > 0;
+  uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
+  uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
+  if (e == hipSuccess && has_shared)
+    e = run_shared(L, x, T, (uint16_t *)at(o.shared_act), shared_out, z, s);
+  mark();
+  // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
+  if (e == hipSuccess)
+    e = launch_combine(eout, inverse, scores, T, k, H, A >= 64, shared_out, z, sparse, y, s);
+  mark();
+  if (e != hipSuccess) return hip_fail(kBlockOp, e);
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -297,87 +400,30 @@ int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
 
 int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
                             uint16_t *y, void *workspace, size_t workspace_bytes, void *stream) {
-  int rc = check_layer(kBlockOp, layer);
-  if (rc) return rc;
-  if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
-  if (tokens == 0) return ok();
-  if (!x || !y) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "hidden states and output must be non-null");
-  const astro_moe_layer &L = *layer;
-  const Layout o = block_layout(L, tokens);
-  if (!workspace || workspace_bytes < o.total) return workspace_fail(kBlockOp, o.total, workspace ? workspace_bytes : 0);
-  hipStream_t s = (hipStream_t)stream;
-  char *ws = (char *)workspace;
-  auto at = [&](size_t off) { return (void *)(ws + off); };
-  const int T = tokens, H = L.hidden, E = L.num_experts, k = L.top_k, I = L.intermediate;
-  const int A = T * k;
-  uint16_t *logits = (uint16_t *)at(o.logits);
-  uint32_t *idx = (uint32_t *)at(o.idx);
-  uint16_t *scores = (uint16_t *)at(o.scores);
-  uint32_t *sorted_order = (uint32_t *)at(o.sorted_order);
-  uint32_t *inverse = (uint32_t *)at(o.inverse);
-  uint32_t *sorted_ids = (uint32_t *)at(o.sorted_ids);
-  uint32_t *offsets = (uint32_t *)at(o.offsets);
-  uint32_t *tile_expert = (uint32_t *)at(o.tile_expert);
-  uint32_t *tile_row0 = (uint32_t *)at(o.tile_row0);
-  uint32_t *tile_count = (uint32_t *)at(o.tile_count);
-  uint16_t *act = (uint16_t *)at(o.act);
-  uint16_t *eout = (uint16_t *)at(o.eout);
-  uint16_t *sparse = (uint16_t *)at(o.sparse);
+  return run_block(layer, x, tokens, y, workspace, workspace_bytes, stream, nullptr);
+}
 
-  hipError_t e = run_router(L, x, T, logits, s);
-  if (e == hipSuccess) e = launch_route_topk(logits, T, E, k, L.normalize_top_k, idx, scores, s);
-  if (e == hipSuccess)
-    e = launch_sort(idx, A, E, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
-                    tile_count, s);
-  if (e != hipSuccess) return hip_fail(kBlockOp, e);
-
-  // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / k]
-  GemmArgs gu{};
-  gu.A = x;
-  gu.lda = H;
-  gu.a_rows = sorted_order;
-  gu.a_div = k;
-  gu.K = H;
-  gu.N = I;
-  if (L.gate_up.w)
-    set_weights(gu, L.gate_up, &L.gate_up, I);
-  else
-    set_weights(gu, L.gate, &L.up, 0);
-  gu.tile_expert = tile_expert;
-  gu.tile_row0 = tile_row0;
-  gu.tile_count = tile_count;
-  gu.expert_offsets = offsets;
-  gu.max_tiles = o.max_tiles;
-  gu.C = act;
-  gu.ldc = I;
-  e = launch_grouped_gemm(gu, kEpiSwiglu, s);
-
-  GemmArgs dn{};
-  dn.A = act;
-  dn.lda = I;
-  dn.a_div = 1;
-  dn.K = I;
-  dn.N = H;
-  set_weights(dn, L.down, nullptr, 0);
-  dn.tile_expert = tile_expert;
-  dn.tile_row0 = tile_row0;
-  dn.tile_count = tile_count;
-  dn.expert_offsets = offsets;
-  dn.max_tiles = o.max_tiles;
-  dn.C = eout;
-  dn.ldc = H;
-  if (e == hipSuccess) e = launch_grouped_gemm(dn, kEpiPlain, s);
-
-  const bool has_shared = L.shared_intermediate > 0;
-  uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
-  uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
-  if (e == hipSuccess && has_shared)
-    e = run_shared(L, x, T, (uint16_t *)at(o.shared_act), shared_out, z, s);
-  // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
-  if (e == hipSuccess)
-    e = launch_combine(eout, inverse, scores, T, k, H, A >= 64, shared_out, z, sparse, y, s);
-  if (e != hipSuccess) return hip_fail(kBlockOp, e);
-  return ok();
+int astro_moe_block_forward_attributed(const astro_moe_layer *layer, const uint16_t *x,
+                                       int32_t tokens, uint16_t *y, void *workspace,
+                                       size_t workspace_bytes, void *stream, float *stage_ms) {
+  if (!stage_ms) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "stage time output must be non-null");
+  hipEvent_t marks[ASTRO_MOE_STAGES + 1];
+  for (int i = 0; i <= ASTRO_MOE_STAGES; ++i) {
+    hipError_t e = hipEventCreate(&marks[i]);
+    if (e != hipSuccess) {
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(marks[j]);
+      return hip_fail(kBlockOp, e);
+    }
+  }
+  int rc = run_block(layer, x, tokens, y, workspace, workspace_bytes, stream, marks);
+  if (rc == ASTRO_MOE_OK) {
+    hipError_t e = hipEventSynchronize(marks[ASTRO_MOE_STAGES]);
+    for (int i = 0; i < ASTRO_MOE_STAGES && e == hipSuccess; ++i)
+      e = hipEventElapsedTime(&stage_ms[i], marks[i], marks[i + 1]);
+    if (e != hipSuccess) rc = hip_fail(kBlockOp, e);
+  }
+  for (int i = 0; i <= ASTRO_MOE_STAGES; ++i) (void)hipEventDestroy(marks[i]);
+  return rc == ASTRO_MOE_OK ? ok() : rc;
 }
 
 int astro_moe_router_logits(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,

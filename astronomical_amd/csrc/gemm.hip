@@ -104,14 +104,14 @@ __device__ __forceinline__ void store_b(uint16_t *dst, const BRegs &r, bool vali
   d[3] = out[3];
 }
 
-template <int KIND, int EPI>
+template <int KIND, int EPI, bool GROUPED>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDSP];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[BR * LDSP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   int expert = 0, row0, m_valid;
-  if (p.tile_expert) {
+  if (GROUPED) {
     const int tile = blockIdx.x;
     if (tile >= (int)*p.tile_count) return;
     expert = (int)p.tile_expert[tile];
@@ -247,22 +247,27 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs p) {
   }
 }
 
-template <int KIND>
+template <int KIND, bool GROUPED>
 hipError_t launch_kind(const GemmArgs &a, int epi, hipStream_t s) {
   const int ntiles = epi == kEpiSwiglu ? (a.N + 63) / 64 : (a.N + BR - 1) / BR;
-  int mt = a.tile_expert ? a.max_tiles : (a.M + BM - 1) / BM;
+  int mt = GROUPED ? a.max_tiles : (a.M + BM - 1) / BM;
   if (mt <= 0 || ntiles <= 0) return hipSuccess;
   // all column tiles of one row tile land on the same XCD (blocks are dealt to the 8
   // XCDs round-robin by linear id) when the row-tile count is a multiple of 8
   mt = (mt + 7) & ~7;
   dim3 grid(mt, ntiles), block(256);
   if (epi == kEpiSwiglu)
-    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiSwiglu>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiSwiglu, GROUPED>), grid, block, 0, s, a);
   else if (epi == kEpiBias)
-    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiBias>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiBias, GROUPED>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiPlain>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiPlain, GROUPED>), grid, block, 0, s, a);
   return hipGetLastError();
+}
+
+template <int KIND>
+hipError_t launch_kind(const GemmArgs &a, int epi, hipStream_t s) {
+  return a.tile_expert ? launch_kind<KIND, true>(a, epi, s) : launch_kind<KIND, false>(a, epi, s);
 }
 
 }  // namespace

@@ -320,6 +320,18 @@ class MoeBlock:
 
     __call__ = forward
 
+    def forward_attributed(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                           workspace: Optional[torch.Tensor] = None):
+        """forward plus per-stage device milliseconds (synchronises the stream)."""
+        x2 = x.contiguous().view(torch.bfloat16).reshape(-1, self.weights.hidden)
+        T = x2.shape[0]
+        y = out if out is not None else torch.empty_like(x2)
+        ws = workspace if workspace is not None else self.workspace(T)
+        ms = (C.c_float * len(_lib.STAGES))()
+        call("astro_moe_block_forward_attributed", C.byref(self._struct), _ptr(x2), T, _ptr(y),
+             _ptr(ws), ws.numel(), _stream(self.device), ms)
+        return y, dict(zip(_lib.STAGES, [float(v) for v in ms]))
+
     def trace(self, tokens: int, workspace: Optional[torch.Tensor] = None) -> dict:
         """Intermediates of the last forward with `tokens` tokens (host numpy copies)."""
         v = WorkspaceView()

@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MoE block (BASELINE.json metric).
+
+Headline (`value`): MoE-layer decode tokens/s at B=1 on the Qwen3.6-35B-A3B-shaped layer
+(config c1: H2048, E256, top-8, I512, shared 512, 4-bit g64).  A step pushes one fresh
+token through a chain of `--layers` distinct seeded layers (40 x 453 MB of expert pages,
+so the step's ~640 MB of selected pages come from HBM, not the 256 MB Infinity Cache);
+each step is one captured HIP graph.  value = layers * steps / timed seconds.
+
+Also reported: prefill of 2048 tokens (config c2) with per-stage times, the roofline of
+the dominant kernel (per-stage hipEvents over the timed workload), and the CPU oracle
+(C restatement of the reference op graph) timed on a bounded sample on the host cores.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--layers", type=int, default=40)
+    p.add_argument("--prefill-iters", type=int, default=20)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the MoE block's multi-GPU "
+                          "sharding (expert parallelism over RCCL) is designed, not built; "
+                          "run with --gpus 1"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from astronomical_amd import configs as CF
+    from astronomical_amd import device_synthetic as DS
+    from astronomical_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = CF.C1
+    nL, K, W = args.layers, args.steps, args.warmup
+
+    # ---------------------------------------------------------------- decode chain
+    layers = [DS.make_layer_device(cfg, layer=l) for l in range(nL)]
+    log(f"generated {nL} layers of {cfg.name}")
+    blocks = [ops.MoeBlock(L) for L in layers]
+    ws = blocks[0].workspace(2048)
+    for b in blocks:
+        b._ws = ws
+    toks = DS.make_tokens_device(cfg, (K + W) * nL, step=1).reshape(K + W, nL, 1, cfg.hidden)
+    outs = torch.empty(nL, 1, cfg.hidden, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+
+    def run_step(s):
+        for l in range(nL):
+            blocks[l].forward(toks[s, l], out=outs[l], workspace=ws)
+
+    # eager reference of step 0, then capture one graph per step
+    run_step(0)
+    torch.cuda.synchronize()
+    eager0 = outs.clone()
+    graphs = []
+    for s in range(K + W):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run_step(s)
+        graphs.append(g)
+    # replays must reproduce eager results, with eager work in between
+    for _ in range(3):
+        outs.zero_()
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outs, eager0), "graph replay differs from eager execution"
+        run_step(1)
+        torch.cuda.synchronize()
+
+    log(f"captured {K + W} step graphs; replay == eager")
+    for s in range(W):
+        graphs[s].replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    t0 = time.perf_counter()
+    ev[0].record()
+    for i in range(K):
+        graphs[W + i].replay()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(K)]
+    total_ms = ev[0].elapsed_time(ev[K])
+    ms_per_step = total_ms / K
+    ms_per_layer = ms_per_step / nL
+    decode_tps = 1000.0 / ms_per_layer  # B = 1 token per layer step
+    page = cfg.page_bytes
+    credited = (cfg.top_k + 1) * page  # U = 8 distinct routed experts + the shared expert
+    layer_gbs = credited / (ms_per_layer * 1e-3) / 1e9
+
+    log(f"decode: {ms_per_layer * 1000:.2f} us/layer")
+    # per-stage device times of the same decode workload (eager, event-bracketed stages)
+    stage_acc = {}
+    for s in range(W, W + min(K, 5)):
+        for l in range(nL):
+            _, st = blocks[l].forward_attributed(toks[s, l], out=outs[l], workspace=ws)
+            for kname, v in st.items():
+                stage_acc.setdefault(kname, []).append(v)
+    stage_ms = {kname: statistics.mean(v) for kname, v in stage_acc.items()}
+    dom = max(("gate_up", "down"), key=lambda s_: stage_ms[s_])
+    # algorithmic bytes of one launch of the dominant kernel at B=1: 8 routed pages
+    H, I, g, b = cfg.hidden, cfg.intermediate, cfg.group_size, cfg.bits
+    per_elem = b / 8 + 4 / g
+    dom_bytes = cfg.top_k * (2 * I * H if dom == "gate_up" else H * I) * per_elem
+    dom_gbs = dom_bytes / (stage_ms[dom] * 1e-3) / 1e9
+
+    # ---------------------------------------------------------------- prefill 2048 (c2)
+    T = 2048
+    xp = DS.make_tokens_device(CF.C2, T)
+    yp = torch.empty_like(xp)
+    blk0 = blocks[0]
+    wsp = blk0.workspace(T)
+    for _ in range(3):
+        blk0.forward(xp, out=yp, workspace=wsp)
+    torch.cuda.synchronize()
+    pe0, pe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    pe0.record()
+    for _ in range(args.prefill_iters):
+        blk0.forward(xp, out=yp, workspace=wsp)
+    pe1.record()
+    torch.cuda.synchronize()
+    prefill_ms = pe0.elapsed_time(pe1) / args.prefill_iters
+    prefill_flops = cfg.flops_per_token() * T
+    pst = {}
+    for _ in range(5):
+        _, st = blk0.forward_attributed(xp, out=yp, workspace=wsp)
+        for kname, v in st.items():
+            pst.setdefault(kname, []).append(v)
+    prefill_stage_ms = {kname: statistics.median(v) for kname, v in pst.items()}
+    log(f"prefill: {prefill_ms * 1000:.1f} us")
+
+    # ---------------------------------------------------------------- CPU baseline
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(layers[0], toks, cfg, args.cpu_seconds)
+
+    result = {
+        "metric": "MoE-layer tokens/s (decode B=1, prefill 2048) + % HBM/MFMA roofline, 1xMI355X",
+        "value": round(decode_tps, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"c1 decode B=1: Qwen3.6-35B-A3B-shaped MoE layer (H2048 E256 top-8 I512 + shared 512, "
+                        f"4-bit g64), one token per step through a chain of {nL} distinct seeded layers, "
+                        f"one hipGraph per step",
+            "layers_per_step": nL,
+            "ms_per_layer": round(ms_per_layer, 5),
+            "step_ms_median": round(statistics.median(step_ms), 4),
+            "wall_s_timed": round(wall, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"grouped_gemm ({dom}) at decode B=1",
+            "achieved": round(dom_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": int(dom_bytes),
+            "avg_launch_us": round(stage_ms[dom] * 1000, 2),
+        },
+        "layer_roofline": {
+            "credited_bytes_per_layer": int(credited),
+            "achieved_GBps": round(layer_gbs, 1),
+            "frac_of_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
+        },
+        "decode_stage_us": {k_: round(v * 1000, 2) for k_, v in stage_ms.items()},
+        "prefill": {
+            "workload": "c2: c1 shapes, 2048 tokens, sorted path",
+            "ms": round(prefill_ms, 4),
+            "tokens_per_s": round(T / (prefill_ms * 1e-3), 1),
+            "achieved_TFLOPs": round(prefill_flops / (prefill_ms * 1e-3) / 1e12, 2),
+            "frac_of_bf16_peak": round(prefill_flops / (prefill_ms * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 4),
+            "stage_us": {k_: round(v * 1000, 2) for k_, v in prefill_stage_ms.items()},
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result))
+
+
+def cpu_baseline(layer_dev, toks, cfg, seconds):
+    """The oracle on the host cores, decode B=1 on a bounded sample of the same tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    import torch
+    from astronomical_amd.ops import bf16_to_numpy, u32_to_numpy
+
+    def host(a):
+        return u32_to_numpy(a) if a.dtype == torch.int32 else bf16_to_numpy(a)
+    Lh = layer_dev.map(host)
+    cores = min(16, os.cpu_count() or 1)
+    oracle.set_threads(cores)
+    xs = bf16_to_numpy(toks.reshape(-1, cfg.hidden))
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds and n < xs.shape[0]:
+        oracle.moe_block_forward(Lh, xs[n:n + 1])
+        n += 1
+    el = time.perf_counter() - t0
+    return {"value": round(n / el, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"c1 decode B=1, {n} tokens through layer 0 (oracle C restatement, "
+                      f"OpenMP over output rows), {el:.1f} s"}
+
+
+if __name__ == "__main__":
+    main()

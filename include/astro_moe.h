@@ -127,6 +127,20 @@ int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int
                             uint16_t *y, void *workspace, size_t workspace_bytes,
                             void *stream);
 
+/*
+ * The same forward with per-stage device times, the counterpart of the reference's
+ * PerformanceAttribution operation timers (crates/model-serving/src/performance_attribution.rs:1-80,
+ * performance_attribution/catalog.rs:54,89-91) — but measuring device time (hipEvents
+ * at stage boundaries) rather than graph construction.  stage_ms[ASTRO_MOE_STAGES]
+ * receives: router projection, route (softmax/top-k), sort (assignment preparation),
+ * gate/up + SwiGLU, down (gathered expert execution), shared expert, combine (weighted
+ * reduction).  Synchronises the stream; not for the hot path.
+ */
+#define ASTRO_MOE_STAGES 7
+int astro_moe_block_forward_attributed(const astro_moe_layer *layer, const uint16_t *x,
+                                       int32_t tokens, uint16_t *y, void *workspace,
+                                       size_t workspace_bytes, void *stream, float *stage_ms);
+
 /* Router projection logits = x·W_rᵀ (bf16 out, fp32 accumulate), plus router_bias if
  * set: forward.rs:52-93 (matmul or quantized_linear). */
 int astro_moe_router_logits(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
