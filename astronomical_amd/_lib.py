@@ -43,7 +43,7 @@ class Layer(C.Structure):
 class WorkspaceView(C.Structure):
     _fields_ = [("total_bytes", C.c_size_t), ("sorted_path", C.c_int32)] + [
         (n, C.c_size_t) for n in ("logits", "indices", "scores", "sorted_order", "inverse_order",
-                                  "sorted_ids", "expert_offsets", "activated", "expert_out",
+                                  "sorted_ids", "expert_offsets", "activated", "activated_ld", "expert_out",
                                   "sparse", "shared_out", "shared_gate_logits")]
 
 

@@ -2,6 +2,7 @@
 // messages), the workspace layout, and the launch sequence of the block.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -106,14 +107,32 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Layout {
   size_t logits, idx, scores, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
-      tile_count, act, eout, sparse, shared_act, shared_out, z, total;
+      tile_count, act, eout, sparse, shared_act, shared_out, z, groups, total;
   int max_tiles;
+  bool decode;     // wavefront-GEMV path: act / eout hold A routed rows then T shared rows
+  int64_t act_ld;  // row length of act
 };
+
+// The decode path takes small batches: at most 8 tokens and 64 assignments, a dense router,
+// and shapes its per-lane register tiles cover (decode.hip: decode_supported).
+bool decode_path(const astro_moe_layer &L, int T) {
+  const int Is = L.shared_intermediate > 0 ? L.shared_intermediate : 0;
+  const int mt = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8;
+  const astro_moe_affine &gu = L.gate_up.w ? L.gate_up : L.gate;
+  return T >= 1 && T <= 8 && T * L.top_k <= 64 && L.router_w != nullptr && L.hidden <= 4096 &&
+         L.intermediate <= 1024 && Is <= 1024 && (gu.bits == 4 || gu.bits == 8) &&
+         (L.down.bits == 4 || L.down.bits == 8) &&
+         (Is == 0 || L.shared_down.bits == L.down.bits) &&
+         // the down kernel keeps every token's activation chunks in registers
+         (L.intermediate <= 512 || mt <= 4);
+}
 
 Layout block_layout(const astro_moe_layer &L, int T) {
   Layout o{};
   const size_t A = (size_t)T * L.top_k, E = (size_t)L.num_experts;
-  o.max_tiles = sort_max_tiles((int)A, (int)E);
+  const size_t Is = L.shared_intermediate > 0 ? (size_t)L.shared_intermediate : 0;
+  o.decode = decode_path(L, T);
+  o.max_tiles = o.decode ? 0 : sort_max_tiles((int)A, (int)E);
   size_t p = 0;
   auto take = [&](size_t bytes) {
     const size_t at = p;
@@ -127,16 +146,27 @@ Layout block_layout(const astro_moe_layer &L, int T) {
   o.inverse = take(A * 4);
   o.sorted_ids = take(A * 4);
   o.offsets = take((E + 2) * 4);
-  o.tile_expert = take((size_t)o.max_tiles * 4);
-  o.tile_row0 = take((size_t)o.max_tiles * 4);
-  o.tile_count = take(4);
-  o.act = take(A * (size_t)L.intermediate * 2);
-  o.eout = take(A * (size_t)L.hidden * 2);
-  o.sparse = take((size_t)T * L.hidden * 2);
-  const size_t Is = L.shared_intermediate > 0 ? (size_t)L.shared_intermediate : 0;
-  o.shared_act = take((size_t)T * Is * 2);
-  o.shared_out = take(Is ? (size_t)T * L.hidden * 2 : 0);
-  o.z = take(Is ? (size_t)T * 2 : 0);
+  if (o.decode) {
+    // n_groups, then expert / first row / count of up to 64 groups
+    o.groups = take(4 + 3 * 64 * 4);
+    o.act_ld = std::max<int64_t>(L.intermediate, (int64_t)Is);
+    o.act = take((A + (Is ? T : 0)) * (size_t)o.act_ld * 2);
+    o.eout = take((A + (Is ? T : 0)) * (size_t)L.hidden * 2);
+    o.sparse = take((size_t)T * L.hidden * 2);
+    o.shared_out = Is ? o.eout + A * (size_t)L.hidden * 2 : 0;
+    o.z = take(Is ? (size_t)T * 2 : 0);
+  } else {
+    o.tile_expert = take((size_t)o.max_tiles * 4);
+    o.tile_row0 = take((size_t)o.max_tiles * 4);
+    o.tile_count = take(4);
+    o.act_ld = L.intermediate;
+    o.act = take(A * (size_t)L.intermediate * 2);
+    o.eout = take(A * (size_t)L.hidden * 2);
+    o.sparse = take((size_t)T * L.hidden * 2);
+    o.shared_act = take((size_t)T * Is * 2);
+    o.shared_out = take(Is ? (size_t)T * L.hidden * 2 : 0);
+    o.z = take(Is ? (size_t)T * 2 : 0);
+  }
   o.total = p;
   return o;
 }
@@ -295,6 +325,101 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   auto mark = [&]() {
     if (marks) (void)hipEventRecord(marks[stage++], s);
   };
+  const bool has_shared = L.shared_intermediate > 0;
+  uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
+  uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
+
+  if (o.decode) {
+    DecodeArgs d{};
+    d.T = T;
+    d.A = A;
+    d.H = H;
+    d.E = E;
+    d.k = k;
+    d.I = I;
+    d.Is = has_shared ? L.shared_intermediate : 0;
+    d.normalize = L.normalize_top_k;
+    d.x = x;
+    d.router_w = L.router_w;
+    d.router_bias = L.router_bias;
+    const astro_moe_affine &g = L.gate_up.w ? L.gate_up : L.gate;
+    const astro_moe_affine &u = L.gate_up.w ? L.gate_up : L.up;
+    const int64_t up_off = L.gate_up.w ? (int64_t)I : 0;
+    d.gu_w_rs = words_per_row(g);
+    d.gu_sb_rs = groups_per_row(g);
+    d.gu_w_es = (int64_t)g.out_features * d.gu_w_rs;
+    d.gu_sb_es = (int64_t)g.out_features * d.gu_sb_rs;
+    d.gate_w = g.w;
+    d.gate_s = g.scales;
+    d.gate_b = g.biases;
+    d.up_w = u.w + up_off * d.gu_w_rs;
+    d.up_s = u.scales + up_off * d.gu_sb_rs;
+    d.up_b = u.biases + up_off * d.gu_sb_rs;
+    d.gu_bits = g.bits;
+    d.gu_group = g.group_size;
+    d.down_w = L.down.w;
+    d.down_s = L.down.scales;
+    d.down_b = L.down.biases;
+    d.dn_w_rs = words_per_row(L.down);
+    d.dn_sb_rs = groups_per_row(L.down);
+    d.dn_w_es = (int64_t)H * d.dn_w_rs;
+    d.dn_sb_es = (int64_t)H * d.dn_sb_rs;
+    d.dn_bits = L.down.bits;
+    d.dn_group = L.down.group_size;
+    if (has_shared) {
+      d.sg_w = L.shared_gate.w;
+      d.sg_s = L.shared_gate.scales;
+      d.sg_b = L.shared_gate.biases;
+      d.su_w = L.shared_up.w;
+      d.su_s = L.shared_up.scales;
+      d.su_b = L.shared_up.biases;
+      d.sg_w_rs = words_per_row(L.shared_gate);
+      d.sg_sb_rs = groups_per_row(L.shared_gate);
+      d.sg_bits = L.shared_gate.bits;
+      d.sg_group = L.shared_gate.group_size;
+      d.sd_w = L.shared_down.w;
+      d.sd_s = L.shared_down.scales;
+      d.sd_b = L.shared_down.biases;
+      d.sd_w_rs = words_per_row(L.shared_down);
+      d.sd_sb_rs = groups_per_row(L.shared_down);
+      d.sd_bits = L.shared_down.bits;
+      d.sd_group = L.shared_down.group_size;
+      d.sz_w = L.shared_expert_gate.w;
+      d.sz_s = L.shared_expert_gate.scales;
+      d.sz_b = L.shared_expert_gate.biases;
+      d.sz_bits = L.shared_expert_gate.bits;
+      d.sz_group = L.shared_expert_gate.group_size;
+    }
+    d.logits = logits;
+    d.scores = scores;
+    d.idx = idx;
+    d.sorted_order = sorted_order;
+    d.inverse_order = inverse;
+    d.sorted_ids = sorted_ids;
+    d.offsets = offsets;
+    uint32_t *groups = (uint32_t *)at(o.groups);
+    d.n_groups = groups;
+    d.g_expert = groups + 1;
+    d.g_start = groups + 1 + 64;
+    d.g_count = groups + 1 + 128;
+    d.act = act;
+    d.act_ld = o.act_ld;
+    d.down_out = eout;
+    d.z = z;
+    d.router_blocks = (E + 3) / 4;
+    d.shared_pair_blocks = has_shared ? (d.Is + 15) / 16 : 0;
+    d.max_groups = std::min(A, E);
+    if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
+    hipError_t e = launch_decode_block(d, s, marks);
+    stage = 5;
+    mark();  // the shared expert ran inside the router and down kernels
+    if (e == hipSuccess)
+      e = launch_combine(eout, inverse, scores, T, k, H, A >= 64, shared_out, z, sparse, y, s);
+    mark();
+    if (e != hipSuccess) return hip_fail(kBlockOp, e);
+    return ok();
+  }
+
   mark();
   hipError_t e = run_router(L, x, T, logits, s);
   mark();
@@ -345,9 +470,6 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   if (e == hipSuccess) e = launch_grouped_gemm(dn, kEpiPlain, s);
   mark();
 
-  const bool has_shared = L.shared_intermediate > 0;
-  uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
-  uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
   if (e == hipSuccess && has_shared)
     e = run_shared(L, x, T, (uint16_t *)at(o.shared_act), shared_out, z, s);
   mark();
@@ -391,6 +513,7 @@ int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
   view->sorted_ids = o.sorted_ids;
   view->expert_offsets = o.offsets;
   view->activated = o.act;
+  view->activated_ld = (size_t)o.act_ld;
   view->expert_out = o.eout;
   view->sparse = o.sparse;
   view->shared_out = o.shared_out;

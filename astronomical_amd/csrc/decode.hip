@@ -1,0 +1,514 @@
+// Decode path of the block (T <= 8 tokens, T*k <= 64 assignments): wavefront GEMVs
+// instead of MFMA tiles.  Per layer:
+//   D1  router GEMV (one wave per expert row) + the shared expert's gate/up + SwiGLU and
+//       its output gate — all the work that does not depend on routing;
+//   D2  route: softmax/top-k per token, the sort of the <= 64 assignments and the table of
+//       distinct experts (one workgroup);
+//   D3  routed gate/up GEMV + SwiGLU: one wave per 4 (gate row, up row) pairs of one
+//       selected expert, every token routed to it;
+//   D4  down GEMV for the routed experts and the shared expert (16 lanes per row, 64 rows
+//       per wave);
+//   then the weighted combine (launch_combine).
+// Affine rows are read once per distinct expert with 16 B per lane loads.  4-bit codes are
+// turned into bf16 pairs (128 + q) with one and/or per pair and multiplied by
+// v_dot2_f32_bf16; the per-group affine terms are applied per 32-input chunk:
+//   sum_j x_j (s q_j + b) = s * sum_j (128 + q_j) x_j + (b - 128 s) * sum_j x_j.
+#include "common.h"
+#include "kernels.h"
+#include "route_dev.h"
+
+namespace astro {
+
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
+                                         c, false);
+}
+
+__device__ __forceinline__ uint32_t pack_bf2_hw(float lo, float hi) {
+  bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// 32 consecutive activations of one token, ready for the code dot products.  For 4-bit
+// codes the bf16 pairs are (x0,x4),(x1,x5),(x2,x6),(x3,x7) per 8 inputs, matching the
+// nibble pairs produced by (word >> 4m) & 0x000f000f; 8-bit codes use natural pairs.
+struct XChunk {
+  uint32_t p[16];
+  float sum;
+};
+
+template <int BITS>
+__device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *src) {
+  uint32_t r[16];
+  const u32x4 *q = (const u32x4 *)src;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 v = q[i];
+    r[4 * i] = v[0];
+    r[4 * i + 1] = v[1];
+    r[4 * i + 2] = v[2];
+    r[4 * i + 3] = v[3];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s = dot2(r[j], 0x3f803f80u, s);
+  xc.sum = s;
+  if (BITS == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t a = r[4 * i], b = r[4 * i + 1], c = r[4 * i + 2], d = r[4 * i + 3];
+      xc.p[4 * i + 0] = (a & 0xffffu) | (c << 16);
+      xc.p[4 * i + 1] = (a >> 16) | (c & 0xffff0000u);
+      xc.p[4 * i + 2] = (b & 0xffffu) | (d << 16);
+      xc.p[4 * i + 3] = (b >> 16) | (d & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) xc.p[j] = r[j];
+  }
+}
+
+// codes of one 32-input chunk of one weight row: 4 words (4-bit) or 8 words (8-bit)
+struct WChunk {
+  u32x4 q[2];
+  float s, b;
+};
+
+template <int BITS>
+__device__ __forceinline__ void load_wchunk(WChunk &w, const uint32_t *row, const uint16_t *srow,
+                                            const uint16_t *brow, int chunk, int group) {
+  const u32x4 *p = (const u32x4 *)(row + chunk * BITS);
+  w.q[0] = p[0];
+  if (BITS == 8) w.q[1] = p[1];
+  const int g = (chunk * 32) / group;
+  w.s = bf2f(srow[g]);
+  w.b = bf2f(brow[g]);
+}
+
+// sum over the chunk of x * (s*q + b)
+template <int BITS>
+__device__ __forceinline__ float chunk_dot(const WChunk &w, const XChunk &x) {
+  float acc = 0.0f;
+  if (BITS == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t word = w.q[0][i];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        acc = dot2(((word >> (4 * m)) & 0x000f000fu) | 0x43004300u, x.p[4 * i + m], acc);
+    }
+    return __builtin_fmaf(w.s, acc, __builtin_fmaf(-128.0f, w.s, w.b) * x.sum);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t word = w.q[i >> 2][i & 3];
+      const uint32_t lo = pack_bf2_hw((float)(word & 255u), (float)((word >> 8) & 255u));
+      const uint32_t hi = pack_bf2_hw((float)((word >> 16) & 255u), (float)(word >> 24));
+      acc = dot2(lo, x.p[2 * i], acc);
+      acc = dot2(hi, x.p[2 * i + 1], acc);
+    }
+    return __builtin_fmaf(w.s, acc, w.b * x.sum);
+  }
+}
+
+// sum over the 16 lanes of a quarter-wave (lanes 16q .. 16q+15)
+__device__ __forceinline__ float quarter_sum(float v) {
+#pragma clang fp contract(off)
+  for (int off = 8; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// One wave: RP consecutive rows of a gate projection and the matching rows of an up
+// projection (SwiGLU) — or of one plain projection — against m <= MT activation rows.
+// Lane l covers input chunks l, l+64 (K <= 4096).
+template <int BITS, int MT, int RP, bool SWIGLU>
+__device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb,
+                                          const uint32_t *uw, const uint16_t *us, const uint16_t *ub,
+                                          int64_t w_rs, int64_t sb_rs, int nrows, int K, int group,
+                                          const uint16_t *x, int64_t ldx, const int *xrows, int m,
+                                          uint16_t *out, int64_t ldo, const int *orows) {
+  const int lane = (int)(threadIdx.x & 63);
+  const int nchunks = K / 32;
+  float accg[RP][MT], accu[RP][MT];
+#pragma unroll
+  for (int r = 0; r < RP; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) accg[r][t] = accu[r][t] = 0.0f;
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) {
+    const int c = lane + 64 * cc;
+    if (c >= nchunks) break;
+    WChunk wg[RP], wu[RP];
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+      if (r < nrows) {
+        load_wchunk<BITS>(wg[r], gw + r * w_rs, gs + r * sb_rs, gb + r * sb_rs, c, group);
+        if (SWIGLU) load_wchunk<BITS>(wu[r], uw + r * w_rs, us + r * sb_rs, ub + r * sb_rs, c, group);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      if (t < m) {
+        XChunk xc;
+        load_xchunk<BITS>(xc, x + (int64_t)xrows[t] * ldx + c * 32);
+#pragma unroll
+        for (int r = 0; r < RP; ++r) {
+          if (r < nrows) {
+            accg[r][t] += chunk_dot<BITS>(wg[r], xc);
+            if (SWIGLU) accu[r][t] += chunk_dot<BITS>(wu[r], xc);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RP; ++r) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      if (r < nrows && t < m) {
+        const float g = wave_sum(accg[r][t]);
+        float v;
+        uint32_t o;
+        if (SWIGLU) {
+          v = wave_sum(accu[r][t]);
+          o = swiglu_bf(round_bf(g), round_bf(v));
+        } else {
+          o = f2bf(g);
+        }
+        if (lane == 0) out[(int64_t)orows[t] * ldo + r] = (uint16_t)o;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- D1: router + shared
+
+template <int MT>
+__global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeArgs p) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ int rows_sh[8], orows_sh[8];
+  if (threadIdx.x < 8) {
+    rows_sh[threadIdx.x] = threadIdx.x;
+    orows_sh[threadIdx.x] = p.A + threadIdx.x;
+  }
+  __syncthreads();
+  const int b = blockIdx.x;
+  if (b < p.router_blocks) {
+    const int e = b * 4 + wave;
+    if (e >= p.E) return;
+    const uint16_t *w = p.router_w + (int64_t)e * p.H;
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+    for (int c = lane; c < p.H / 32; c += 64) {
+      const u32x4 *wp = (const u32x4 *)(w + c * 32);
+      const u32x4 w0 = wp[0], w1 = wp[1], w2 = wp[2], w3 = wp[3];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        if (t < p.T) {
+          const u32x4 *xp = (const u32x4 *)(p.x + (int64_t)t * p.H + c * 32);
+          const u32x4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+          float a = acc[t];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a = dot2(w0[i], x0[i], a);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a = dot2(w1[i], x1[i], a);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a = dot2(w2[i], x2[i], a);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a = dot2(w3[i], x3[i], a);
+          acc[t] = a;
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      if (t < p.T) {
+        const float v = wave_sum(acc[t]);
+        if (lane == 0) {
+          uint32_t o = f2bf(v);
+          if (p.router_bias) o = f2bf(bf2f(o) + bf2f(p.router_bias[e]));
+          p.logits[(int64_t)t * p.E + e] = (uint16_t)o;
+        }
+      }
+    }
+    return;
+  }
+  const int sb = b - p.router_blocks;
+  if (sb < p.shared_pair_blocks) {
+    // shared expert gate/up + SwiGLU: rows 4*sb.. of [Is]
+    const int r0 = (sb * 4 + wave) * 4;
+    if (r0 >= p.Is) return;
+    const int nrows = min(4, p.Is - r0);
+    if (p.sg_bits == 4)
+      rows_task<4, MT, 4, true>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs, p.sg_b + r0 * p.sg_sb_rs,
+                                p.su_w + r0 * p.sg_w_rs, p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
+                                p.sg_w_rs, p.sg_sb_rs, nrows, p.H, p.sg_group, p.x, p.H, rows_sh,
+                                p.T, p.act + r0, p.act_ld, orows_sh);
+    else
+      rows_task<8, MT, 4, true>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs, p.sg_b + r0 * p.sg_sb_rs,
+                                p.su_w + r0 * p.sg_w_rs, p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
+                                p.sg_w_rs, p.sg_sb_rs, nrows, p.H, p.sg_group, p.x, p.H, rows_sh,
+                                p.T, p.act + r0, p.act_ld, orows_sh);
+    return;
+  }
+  // the shared expert's output gate (one row) -> z[t]
+  if (wave != 0 || !p.sz_w) return;
+  if (p.sz_bits == 4)
+    rows_task<4, MT, 1, false>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1, p.H,
+                               p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
+  else
+    rows_task<8, MT, 1, false>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1, p.H,
+                               p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
+}
+
+// ---------------------------------------------------------------- D2: route + sort
+
+__global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
+  __shared__ uint32_t idx_sh[64], sid_sh[64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int t = wave; t < p.T; t += 4) {
+    uint32_t my_idx, my_score;
+    route_token(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score);
+    if (lane < p.k) {
+      p.idx[t * p.k + lane] = my_idx;
+      p.scores[t * p.k + lane] = (uint16_t)my_score;
+      idx_sh[t * p.k + lane] = my_idx;
+    }
+  }
+  __syncthreads();
+  const int A = p.A;
+  if (wave == 0) {
+    // stable sort of <= 64 assignments by (expert, slot): rank = number of smaller keys
+    const uint32_t key = lane < A ? (idx_sh[lane] << 6) | (uint32_t)lane : 0xffffffffu;
+    uint32_t rank = 0;
+    for (int b2 = 0; b2 < A; ++b2) rank += (uint32_t)__shfl((int)key, b2, kWave) < key;
+    if (lane < A) {
+      p.sorted_order[rank] = (uint32_t)lane;
+      p.inverse_order[lane] = rank;
+      p.sorted_ids[rank] = key >> 6;
+      sid_sh[rank] = key >> 6;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // distinct experts in ascending order: group g = (expert, first sorted row, count)
+    const uint32_t sid = lane < A ? sid_sh[lane] : 0xffffffffu;
+    const bool start = lane < A && (lane == 0 || sid != sid_sh[lane - 1]);
+    const uint64_t mask = __ballot(start);
+    if (start) {
+      const int g = __popcll(mask & ((1ull << lane) - 1ull));
+      const uint64_t above = lane == 63 ? 0ull : (mask >> (lane + 1));
+      const int next = above ? lane + 1 + __ffsll((long long)above) - 1 : A;
+      p.g_expert[g] = sid;
+      p.g_start[g] = (uint32_t)lane;
+      p.g_count[g] = (uint32_t)(next - lane);
+    }
+    if (lane == 0) *p.n_groups = (uint32_t)__popcll(mask);
+  }
+  // expert offsets [E+2] (E+1: trailing out-of-range bucket, empty here)
+  for (int e = threadIdx.x; e <= p.E + 1; e += 256) {
+    uint32_t c = 0;
+    for (int i = 0; i < A; ++i) c += sid_sh[i] < (uint32_t)e;
+    p.offsets[e] = e <= p.E ? c : (uint32_t)A;
+  }
+}
+
+// ---------------------------------------------------------------- D3: routed gate/up
+
+template <int BITS, int MT>
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
+  __shared__ int rows_sh[MT], orows_sh[MT];
+  const int g = blockIdx.y;
+  const int ng = (int)*p.n_groups;
+  if (g >= ng || g >= p.max_groups) return;
+  const uint32_t e = p.g_expert[g], start = p.g_start[g], m = p.g_count[g];
+  if (e >= (uint32_t)p.E || start + m > (uint32_t)p.A || m > (uint32_t)MT || m == 0) return;
+  if (threadIdx.x < m) {
+    const uint32_t tok = p.sorted_order[start + threadIdx.x] / (uint32_t)p.k;
+    rows_sh[threadIdx.x] = (int)(tok < (uint32_t)p.T ? tok : 0u);
+    orows_sh[threadIdx.x] = (int)(start + threadIdx.x);
+  }
+  __syncthreads();
+  const int wave = threadIdx.x >> 6;
+  const int r0 = (blockIdx.x * 4 + wave) * 4;
+  if (r0 >= p.I) return;
+  const int nrows = min(4, p.I - r0);
+  const int64_t wo = (int64_t)e * p.gu_w_es + (int64_t)r0 * p.gu_w_rs;
+  const int64_t so = (int64_t)e * p.gu_sb_es + (int64_t)r0 * p.gu_sb_rs;
+  rows_task<BITS, MT, 4, true>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
+                               p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows, p.H,
+                               p.gu_group, p.x, p.H, rows_sh, (int)m, p.act + r0, p.act_ld,
+                               orows_sh);
+}
+
+// ---------------------------------------------------------------- D4: down (routed + shared)
+
+// One wave per (group, 64 output rows).  Quarter q of the wave takes rows 4*it + q; its 16
+// lanes split the row's input chunks (lane l16 takes chunks l16, l16+16).
+template <int BITS, int MT>
+__global__ __launch_bounds__(64) void decode_down_kernel(const DecodeArgs p) {
+  __shared__ uint16_t res[MT][64];
+  const int lane = threadIdx.x, l16 = lane & 15, q = lane >> 4;
+  const int g = blockIdx.y;
+  const int ng = (int)*p.n_groups;
+  const bool shared = p.Is > 0 && g == ng;
+  if (g > ng || g > p.max_groups || (g == ng && !shared)) return;
+  int rows[MT], m, K, group;
+  const uint32_t *w;
+  const uint16_t *sc, *bi;
+  int64_t w_rs, sb_rs;
+  if (shared) {
+    m = p.T;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) rows[t] = p.A + (t < m ? t : 0);
+    w = p.sd_w;
+    sc = p.sd_s;
+    bi = p.sd_b;
+    w_rs = p.sd_w_rs;
+    sb_rs = p.sd_sb_rs;
+    K = p.Is;
+    group = p.sd_group;
+  } else {
+    const uint32_t e = p.g_expert[g], start = p.g_start[g];
+    m = (int)p.g_count[g];
+    if (e >= (uint32_t)p.E || start + (uint32_t)m > (uint32_t)p.A || m > MT || m <= 0) return;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) rows[t] = (int)start + (t < m ? t : 0);
+    w = p.down_w + (int64_t)e * p.dn_w_es;
+    sc = p.down_s + (int64_t)e * p.dn_sb_es;
+    bi = p.down_b + (int64_t)e * p.dn_sb_es;
+    w_rs = p.dn_w_rs;
+    sb_rs = p.dn_sb_rs;
+    K = p.I;
+    group = p.dn_group;
+  }
+  const int h0 = blockIdx.x * 64;
+  const int nchunks = K / 32;
+  float acc[16][MT];
+#pragma unroll
+  for (int it = 0; it < 16; ++it)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[it][t] = 0.0f;
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) {
+    const int c = l16 + 16 * cc;
+    if (c >= nchunks) break;
+    WChunk wch[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int h = h0 + 4 * it + q;
+      if (h < p.H) load_wchunk<BITS>(wch[it], w + (int64_t)h * w_rs, sc + (int64_t)h * sb_rs,
+                                     bi + (int64_t)h * sb_rs, c, group);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      if (t < m) {
+        XChunk xc;
+        load_xchunk<BITS>(xc, p.act + (int64_t)rows[t] * p.act_ld + c * 32);
+#pragma unroll
+        for (int it = 0; it < 16; ++it)
+          if (h0 + 4 * it + q < p.H) acc[it][t] += chunk_dot<BITS>(wch[it], xc);
+      }
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      if (t < m) {
+        const float v = quarter_sum(acc[it][t]);
+        if (l16 == 0) res[t][4 * it + q] = (uint16_t)f2bf(v);
+      }
+    }
+  }
+  __syncthreads();
+  const int h = h0 + lane;
+  if (h < p.H) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      if (t < m) p.down_out[(int64_t)rows[t] * p.H + h] = res[t][lane];
+  }
+}
+
+template <int BITS, int MT>
+void launch_gate_up_mt(const DecodeArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT>), dim3((a.I + 15) / 16, a.max_groups),
+                     dim3(256), 0, s, a);
+}
+
+template <int BITS, int MT>
+void launch_down_mt(const DecodeArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((decode_down_kernel<BITS, MT>),
+                     dim3((a.H + 63) / 64, a.max_groups + (a.Is > 0 ? 1 : 0)), dim3(64), 0, s, a);
+}
+
+template <int BITS>
+void launch_gate_up(const DecodeArgs &a, int mt, hipStream_t s) {
+  if (mt == 1) launch_gate_up_mt<BITS, 1>(a, s);
+  else if (mt == 2) launch_gate_up_mt<BITS, 2>(a, s);
+  else if (mt == 4) launch_gate_up_mt<BITS, 4>(a, s);
+  else launch_gate_up_mt<BITS, 8>(a, s);
+}
+
+template <int BITS>
+void launch_down(const DecodeArgs &a, int mt, hipStream_t s) {
+  if (mt == 1) launch_down_mt<BITS, 1>(a, s);
+  else if (mt == 2) launch_down_mt<BITS, 2>(a, s);
+  else if (mt == 4) launch_down_mt<BITS, 4>(a, s);
+  else launch_down_mt<BITS, 8>(a, s);
+}
+
+}  // namespace
+
+bool decode_supported(const DecodeArgs &a) {
+  return a.T >= 1 && a.T <= 8 && a.A <= 64 && a.router_w != nullptr && a.H % 32 == 0 &&
+         a.H <= 4096 && a.I % 32 == 0 && a.I <= 1024 && a.Is % 32 == 0 && a.Is <= 1024 &&
+         a.E <= 1024 && a.k <= 64 && (a.gu_bits == 4 || a.gu_bits == 8) &&
+         (a.dn_bits == 4 || a.dn_bits == 8) && a.gu_group >= 32 && a.dn_group >= 32 &&
+         (a.Is == 0 || (a.sd_bits == a.dn_bits && (a.sg_bits == 4 || a.sg_bits == 8) &&
+                        (a.sz_bits == 4 || a.sz_bits == 8)));
+}
+
+hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *marks) {
+  const int mt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8;
+  int stage = 0;
+  auto mark = [&]() {
+    if (marks) (void)hipEventRecord(marks[stage++], s);
+  };
+  // D1: router rows (4 experts per block), shared gate/up (16 rows per block), output gate
+  const int blocks = a.router_blocks + a.shared_pair_blocks + (a.sz_w ? 1 : 0);
+  mark();
+  switch (mt) {
+    case 1: hipLaunchKernelGGL(decode_router_shared_kernel<1>, dim3(blocks), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(decode_router_shared_kernel<2>, dim3(blocks), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(decode_router_shared_kernel<4>, dim3(blocks), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(decode_router_shared_kernel<8>, dim3(blocks), dim3(256), 0, s, a); break;
+  }
+  hipError_t e = hipGetLastError();
+  mark();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(256), 0, s, a);
+  e = hipGetLastError();
+  mark();  // sorting happens inside the route kernel: the sort stage is empty here
+  mark();
+  if (e != hipSuccess) return e;
+  if (a.gu_bits == 8) launch_gate_up<8>(a, mt, s);
+  else launch_gate_up<4>(a, mt, s);
+  e = hipGetLastError();
+  mark();
+  if (e != hipSuccess) return e;
+  if (a.dn_bits == 8) launch_down<8>(a, mt, s);
+  else launch_down<4>(a, mt, s);
+  e = hipGetLastError();
+  mark();
+  return e;
+}
+
+}  // namespace astro

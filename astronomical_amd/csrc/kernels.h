@@ -80,4 +80,33 @@ hipError_t launch_combine_shared(const uint16_t *sparse, const uint16_t *shared_
                                  const uint16_t *gate_logits, int T, int D, uint16_t *y,
                                  hipStream_t s);
 
+// Decode path (T <= 8 tokens, T*k <= 64): every pointer is a device pointer; rows of `act`
+// and `down_out` are the A sorted assignments followed by the T shared-expert rows.
+struct DecodeArgs {
+  int T, A, H, E, k, I, Is, normalize;
+  const uint16_t *x, *router_w, *router_bias;
+  // routed gate/up (fused or separate pages share strides) and down
+  const uint32_t *gate_w, *up_w, *down_w;
+  const uint16_t *gate_s, *gate_b, *up_s, *up_b, *down_s, *down_b;
+  int64_t gu_w_es, gu_w_rs, gu_sb_es, gu_sb_rs;
+  int64_t dn_w_es, dn_w_rs, dn_sb_es, dn_sb_rs;
+  int gu_bits, gu_group, dn_bits, dn_group;
+  // shared expert
+  const uint32_t *sg_w, *su_w, *sd_w, *sz_w;
+  const uint16_t *sg_s, *sg_b, *su_s, *su_b, *sd_s, *sd_b, *sz_s, *sz_b;
+  int64_t sg_w_rs, sg_sb_rs, sd_w_rs, sd_sb_rs;
+  int sg_bits, sg_group, sd_bits, sd_group, sz_bits, sz_group;
+  // workspace
+  uint16_t *logits, *scores;
+  uint32_t *idx, *sorted_order, *inverse_order, *sorted_ids, *offsets;
+  uint32_t *n_groups, *g_expert, *g_start, *g_count;
+  uint16_t *act, *down_out, *z;
+  int64_t act_ld;
+  int router_blocks, shared_pair_blocks, max_groups;
+};
+
+bool decode_supported(const DecodeArgs &a);
+// launches the four decode kernels; marks (nullable) receives 6 stage boundaries
+hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *marks);
+
 }  // namespace astro

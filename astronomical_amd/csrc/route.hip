@@ -2,79 +2,25 @@
 // sort-by-expert permutation (assignment_sort.rs:79-91) with the grouped-GEMM tile table.
 #include "common.h"
 #include "kernels.h"
+#include "route_dev.h"
 
 namespace astro {
 
 namespace {
 
-constexpr int kMaxPerLane = 16;  // experts per lane: E <= 1024
-
-// One wave per token.  Lane j holds experts j, j+64, ...; the softmax denominator is
-// each lane's sequential sum followed by the 64-lane tree (wave_sum), p = bf16(e * 1/S).
-// Top-k: k rounds of a wave-wide maximum over the keys (bf16(p) << 16 | expert); a
-// larger key is a larger probability, ties broken toward the higher expert index, as
-// MLX's (value, index) partition comparator orders them.  Slot k-1-r receives round r,
-// so the slice is ascending in (p, index).
+// One wave per token (route_token in route_dev.h).
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restrict__ logits,
                                                          int T, int E, int k, int normalize,
                                                          uint32_t *__restrict__ idx,
                                                          uint16_t *__restrict__ scores) {
-#pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const uint16_t *l = logits + (int64_t)t * E;
-  const int per = (E + 63) >> 6;
-  float v[kMaxPerLane];
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = (i < per && e < E) ? bf2f(l[e]) : -__builtin_inff();
-    m = fmaxf(m, v[i]);
-  }
-  m = wave_max(m);
-  float part = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = (i < per && e < E) ? det_expf(v[i] - m) : 0.0f;
-    part = part + v[i];
-  }
-  const float rcp = 1.0f / wave_sum(part);
-  uint32_t cand[kMaxPerLane];
-#pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    const int e = lane + 64 * i;
-    // candidates are key + 1 so that 0 means "none / taken"
-    cand[i] = (i < per && e < E) ? (((f2bf(v[i] * rcp) << 16) | (uint32_t)e) + 1u) : 0u;
-  }
-  uint32_t my_idx = 0, my_p = 0;
-  for (int r = 0; r < k; ++r) {
-    uint32_t best = 0;
-#pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i) best = cand[i] > best ? cand[i] : best;
-    const uint32_t key = wave_max_u32(best) - 1u;
-    const uint32_t e = key & 0xffffu;
-    if ((int)(e & 63) == lane) {
-#pragma unroll
-      for (int i = 0; i < kMaxPerLane; ++i)
-        if (i == (int)(e >> 6)) cand[i] = 0u;
-    }
-    if (lane == k - 1 - r) {
-      my_idx = e;
-      my_p = key >> 16;
-    }
-  }
-  float s = bf2f(my_p);
-  if (normalize) {
-    float sum = 0.0f;
-    for (int j = 0; j < k; ++j) sum = sum + __shfl(s, j, kWave);
-    s = s / round_bf(sum);
-  }
+  uint32_t my_idx, my_score;
+  route_token(logits + (int64_t)t * E, E, k, normalize, my_idx, my_score);
   if (lane < k) {
     idx[(int64_t)t * k + lane] = my_idx;
-    scores[(int64_t)t * k + lane] = (uint16_t)f2bf(s);
+    scores[(int64_t)t * k + lane] = (uint16_t)my_score;
   }
 }
 

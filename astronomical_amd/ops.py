@@ -354,7 +354,7 @@ class MoeBlock:
             inverse_order=get(v.inverse_order, A, np.uint32),
             sorted_ids=get(v.sorted_ids, A, np.uint32),
             expert_offsets=get(v.expert_offsets, E + 1, np.uint32),
-            activated_sorted=get(v.activated, A * I, np.uint16).reshape(A, I),
+            activated_sorted=get(v.activated, A * v.activated_ld, np.uint16).reshape(A, v.activated_ld)[:, :I],
             expert_out_sorted=get(v.expert_out, A * H, np.uint16).reshape(A, H),
             sparse=get(v.sparse, T * H, np.uint16).reshape(T, H))
         if L.shared_intermediate:

@@ -102,7 +102,8 @@ typedef struct astro_moe_workspace_view {
   size_t inverse_order;      /* u32 [A]: original slot -> sorted slot */
   size_t sorted_ids;         /* u32 [A] */
   size_t expert_offsets;     /* u32 [E+1] */
-  size_t activated;          /* bf16 [A][I], sorted order */
+  size_t activated;          /* bf16 [A][activated_ld], sorted order */
+  size_t activated_ld;       /* elements per activated row (>= I) */
   size_t expert_out;         /* bf16 [A][H], sorted order */
   size_t sparse;             /* bf16 [T][H] */
   size_t shared_out;         /* bf16 [T][H] */
