@@ -411,8 +411,8 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     d.max_groups = std::min(A, E);
     if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
     hipError_t e = launch_decode_block(d, s, marks);
-    stage = 5;
-    mark();  // the shared expert ran inside the router and down kernels
+    stage = 6;  // launch_decode_block recorded marks[0..5]
+    mark();     // the shared expert ran inside the router and down kernels: empty stage
     if (e == hipSuccess)
       e = launch_combine(eout, inverse, scores, T, k, H, A >= 64, shared_out, z, sparse, y, s);
     mark();
