@@ -117,13 +117,6 @@ __device__ __forceinline__ float chunk_dot(const WChunk &w, const XChunk &x) {
   }
 }
 
-// sum over the 16 lanes of a quarter-wave (lanes 16q .. 16q+15)
-__device__ __forceinline__ float quarter_sum(float v) {
-#pragma clang fp contract(off)
-  for (int off = 8; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
-  return v;
-}
-
 // One wave: RP consecutive rows of a gate projection and the matching rows of an up
 // projection (SwiGLU) — or of one plain projection — against m <= MT activation rows.
 // Lane l covers input chunks l, l+64 (K <= 4096).
@@ -172,11 +165,11 @@ __device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       if (r < nrows && t < m) {
-        const float g = wave_sum(accg[r][t]);
+        const float g = wave_sum_fast(accg[r][t]);
         float v;
         uint32_t o;
         if (SWIGLU) {
-          v = wave_sum(accu[r][t]);
+          v = wave_sum_fast(accu[r][t]);
           o = swiglu_bf(round_bf(g), round_bf(v));
         } else {
           o = f2bf(g);
@@ -230,7 +223,7 @@ __global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeA
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       if (t < p.T) {
-        const float v = wave_sum(acc[t]);
+        const float v = wave_sum_fast(acc[t]);
         if (lane == 0) {
           uint32_t o = f2bf(v);
           if (p.router_bias) o = f2bf(bf2f(o) + bf2f(p.router_bias[e]));
@@ -271,11 +264,11 @@ __global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeA
 // ---------------------------------------------------------------- D2: route + sort
 
 __global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
-  __shared__ uint32_t idx_sh[64], sid_sh[64];
+  __shared__ uint32_t idx_sh[64], sid_sh[64], key_sh[64], lds[4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int t = wave; t < p.T; t += 4) {
     uint32_t my_idx, my_score;
-    route_token(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score);
+    route_token(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score, lds[wave]);
     if (lane < p.k) {
       p.idx[t * p.k + lane] = my_idx;
       p.scores[t * p.k + lane] = (uint16_t)my_score;
@@ -287,8 +280,11 @@ __global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
   if (wave == 0) {
     // stable sort of <= 64 assignments by (expert, slot): rank = number of smaller keys
     const uint32_t key = lane < A ? (idx_sh[lane] << 6) | (uint32_t)lane : 0xffffffffu;
+    key_sh[lane] = key;
+    __builtin_amdgcn_wave_barrier();
     uint32_t rank = 0;
-    for (int b2 = 0; b2 < A; ++b2) rank += (uint32_t)__shfl((int)key, b2, kWave) < key;
+#pragma unroll
+    for (int b2 = 0; b2 < 64; ++b2) rank += key_sh[b2] < key;
     if (lane < A) {
       p.sorted_order[rank] = (uint32_t)lane;
       p.inverse_order[lane] = rank;
@@ -423,7 +419,7 @@ __global__ __launch_bounds__(64) void decode_down_kernel(const DecodeArgs p) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       if (t < m) {
-        const float v = quarter_sum(acc[it][t]);
+        const float v = row_sum(acc[it][t]);
         if (l16 == 0) res[t][4 * it + q] = (uint16_t)f2bf(v);
       }
     }

@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void qgemv_rows_kernel(
       acc = __builtin_fmaf(xv[i], __builtin_fmaf(s, q, b), acc);
     }
   }
-  acc = wave_sum(acc);
+  acc = wave_sum_fast(acc);
   if (lane == 0) out[(int64_t)t * N + n] = (uint16_t)f2bf(acc);
 }
 
