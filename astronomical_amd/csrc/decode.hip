@@ -17,6 +17,8 @@
 #include "kernels.h"
 #include "route_dev.h"
 
+#include <algorithm>
+
 namespace astro {
 
 namespace {
@@ -118,44 +120,50 @@ __device__ __forceinline__ float chunk_dot(const WChunk &w, const XChunk &x) {
 }
 
 // One wave: RP consecutive rows of a gate projection and the matching rows of an up
-// projection (SwiGLU) — or of one plain projection — against m <= MT activation rows.
-// Lane l covers input chunks l, l+64 (K <= 4096).
-template <int BITS, int MT, int RP, bool SWIGLU>
+// projection (SwiGLU) — or of one plain projection — against MT activation rows.  Lane l
+// covers input chunks l, l+64, ... (NC chunks).  The body has no data-dependent branches:
+// rows past `nrows` reuse the last row, `xrows` arrives clamped to valid rows, lanes past
+// the chunk count load chunk 0 and contribute zero, so every load is issued up front.
+template <int BITS, int MT, int RP, bool SWIGLU, int NC>
 __device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb,
                                           const uint32_t *uw, const uint16_t *us, const uint16_t *ub,
-                                          int64_t w_rs, int64_t sb_rs, int nrows, int K, int group,
-                                          const uint16_t *x, int64_t ldx, const int *xrows, int m,
-                                          uint16_t *out, int64_t ldo, const int *orows) {
+                                          int64_t w_rs, int64_t sb_rs, int nrows, int nchunks,
+                                          int group, const uint16_t *x, int64_t ldx,
+                                          const int *xrows, int m, uint16_t *out, int64_t ldo,
+                                          const int *orows) {
   const int lane = (int)(threadIdx.x & 63);
-  const int nchunks = K / 32;
   float accg[RP][MT], accu[RP][MT];
 #pragma unroll
   for (int r = 0; r < RP; ++r)
 #pragma unroll
     for (int t = 0; t < MT; ++t) accg[r][t] = accu[r][t] = 0.0f;
+  int xr[MT];
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
-    const int c = lane + 64 * cc;
-    if (c >= nchunks) break;
+  for (int t = 0; t < MT; ++t) xr[t] = xrows[t];
+#pragma unroll
+  for (int cc = 0; cc < NC; ++cc) {
+    const int craw = lane + 64 * cc;
+    const bool cv = craw < nchunks;
+    const int c = cv ? craw : 0;
     WChunk wg[RP], wu[RP];
 #pragma unroll
     for (int r = 0; r < RP; ++r) {
-      if (r < nrows) {
-        load_wchunk<BITS>(wg[r], gw + r * w_rs, gs + r * sb_rs, gb + r * sb_rs, c, group);
-        if (SWIGLU) load_wchunk<BITS>(wu[r], uw + r * w_rs, us + r * sb_rs, ub + r * sb_rs, c, group);
-      }
+      const int rr = r < nrows ? r : nrows - 1;
+      load_wchunk<BITS>(wg[r], gw + rr * w_rs, gs + rr * sb_rs, gb + rr * sb_rs, c, group);
+      if (SWIGLU) load_wchunk<BITS>(wu[r], uw + rr * w_rs, us + rr * sb_rs, ub + rr * sb_rs, c, group);
     }
+    XChunk xc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) load_xchunk<BITS>(xc[t], x + (int64_t)xr[t] * ldx + c * 32);
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      if (t < m) {
-        XChunk xc;
-        load_xchunk<BITS>(xc, x + (int64_t)xrows[t] * ldx + c * 32);
 #pragma unroll
-        for (int r = 0; r < RP; ++r) {
-          if (r < nrows) {
-            accg[r][t] += chunk_dot<BITS>(wg[r], xc);
-            if (SWIGLU) accu[r][t] += chunk_dot<BITS>(wu[r], xc);
-          }
+      for (int r = 0; r < RP; ++r) {
+        const float dg = chunk_dot<BITS>(wg[r], xc[t]);
+        accg[r][t] += cv ? dg : 0.0f;
+        if (SWIGLU) {
+          const float du = chunk_dot<BITS>(wu[r], xc[t]);
+          accu[r][t] += cv ? du : 0.0f;
         }
       }
     }
@@ -164,34 +172,33 @@ __device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs
   for (int r = 0; r < RP; ++r) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      if (r < nrows && t < m) {
-        const float g = wave_sum_fast(accg[r][t]);
-        float v;
-        uint32_t o;
-        if (SWIGLU) {
-          v = wave_sum_fast(accu[r][t]);
-          o = swiglu_bf(round_bf(g), round_bf(v));
-        } else {
-          o = f2bf(g);
-        }
-        if (lane == 0) out[(int64_t)orows[t] * ldo + r] = (uint16_t)o;
+      const float g = wave_sum_fast(accg[r][t]);
+      uint32_t o;
+      if (SWIGLU) {
+        const float u = wave_sum_fast(accu[r][t]);
+        o = swiglu_bf(round_bf(g), round_bf(u));
+      } else {
+        o = f2bf(g);
       }
+      if (lane == 0 && r < nrows && t < m) out[(int64_t)orows[t] * ldo + r] = (uint16_t)o;
     }
   }
 }
 
 // ---------------------------------------------------------------- D1: router + shared
 
-template <int MT>
+template <int MT, int NC>
 __global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeArgs p) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __shared__ int rows_sh[8], orows_sh[8];
-  if (threadIdx.x < 8) {
-    rows_sh[threadIdx.x] = threadIdx.x;
-    orows_sh[threadIdx.x] = p.A + threadIdx.x;
+  __shared__ int rows_sh[MT], orows_sh[MT];
+  if (threadIdx.x < MT) {
+    const int t = threadIdx.x < p.T ? threadIdx.x : p.T - 1;
+    rows_sh[threadIdx.x] = t;
+    orows_sh[threadIdx.x] = p.A + t;
   }
   __syncthreads();
   const int b = blockIdx.x;
+  const int nchunks = p.H / 32;
   if (b < p.router_blocks) {
     const int e = b * 4 + wave;
     if (e >= p.E) return;
@@ -199,76 +206,81 @@ __global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeA
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-    for (int c = lane; c < p.H / 32; c += 64) {
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const int craw = lane + 64 * cc;
+      const bool cv = craw < nchunks;
+      const int c = cv ? craw : 0;
       const u32x4 *wp = (const u32x4 *)(w + c * 32);
-      const u32x4 w0 = wp[0], w1 = wp[1], w2 = wp[2], w3 = wp[3];
+      u32x4 wv[4], xv[MT][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[i] = wp[i];
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        if (t < p.T) {
-          const u32x4 *xp = (const u32x4 *)(p.x + (int64_t)t * p.H + c * 32);
-          const u32x4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
-          float a = acc[t];
+        const u32x4 *xp = (const u32x4 *)(p.x + (int64_t)rows_sh[t] * p.H + c * 32);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) a = dot2(w0[i], x0[i], a);
+        for (int i = 0; i < 4; ++i) xv[t][i] = xp[i];
+      }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) a = dot2(w1[i], x1[i], a);
+      for (int t = 0; t < MT; ++t) {
+        float a = 0.0f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) a = dot2(w2[i], x2[i], a);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) a = dot2(w3[i], x3[i], a);
-          acc[t] = a;
-        }
+          for (int j = 0; j < 4; ++j) a = dot2(wv[i][j], xv[t][i][j], a);
+        acc[t] += cv ? a : 0.0f;
       }
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      if (t < p.T) {
-        const float v = wave_sum_fast(acc[t]);
-        if (lane == 0) {
-          uint32_t o = f2bf(v);
-          if (p.router_bias) o = f2bf(bf2f(o) + bf2f(p.router_bias[e]));
-          p.logits[(int64_t)t * p.E + e] = (uint16_t)o;
-        }
+      const float v = wave_sum_fast(acc[t]);
+      if (lane == 0 && t < p.T) {
+        uint32_t o = f2bf(v);
+        if (p.router_bias) o = f2bf(bf2f(o) + bf2f(p.router_bias[e]));
+        p.logits[(int64_t)t * p.E + e] = (uint16_t)o;
       }
     }
     return;
   }
   const int sb = b - p.router_blocks;
   if (sb < p.shared_pair_blocks) {
-    // shared expert gate/up + SwiGLU: rows 4*sb.. of [Is]
+    // shared expert gate/up + SwiGLU: rows 16*sb .. of [Is], 4 per wave
     const int r0 = (sb * 4 + wave) * 4;
     if (r0 >= p.Is) return;
     const int nrows = min(4, p.Is - r0);
     if (p.sg_bits == 4)
-      rows_task<4, MT, 4, true>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs, p.sg_b + r0 * p.sg_sb_rs,
-                                p.su_w + r0 * p.sg_w_rs, p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
-                                p.sg_w_rs, p.sg_sb_rs, nrows, p.H, p.sg_group, p.x, p.H, rows_sh,
-                                p.T, p.act + r0, p.act_ld, orows_sh);
+      rows_task<4, MT, 4, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
+                                    p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
+                                    p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs, p.sg_w_rs,
+                                    p.sg_sb_rs, nrows, nchunks, p.sg_group, p.x, p.H, rows_sh, p.T,
+                                    p.act + r0, p.act_ld, orows_sh);
     else
-      rows_task<8, MT, 4, true>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs, p.sg_b + r0 * p.sg_sb_rs,
-                                p.su_w + r0 * p.sg_w_rs, p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
-                                p.sg_w_rs, p.sg_sb_rs, nrows, p.H, p.sg_group, p.x, p.H, rows_sh,
-                                p.T, p.act + r0, p.act_ld, orows_sh);
+      rows_task<8, MT, 4, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
+                                    p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
+                                    p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs, p.sg_w_rs,
+                                    p.sg_sb_rs, nrows, nchunks, p.sg_group, p.x, p.H, rows_sh, p.T,
+                                    p.act + r0, p.act_ld, orows_sh);
     return;
   }
   // the shared expert's output gate (one row) -> z[t]
   if (wave != 0 || !p.sz_w) return;
   if (p.sz_bits == 4)
-    rows_task<4, MT, 1, false>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1, p.H,
-                               p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
+    rows_task<4, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
+                                   nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
   else
-    rows_task<8, MT, 1, false>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1, p.H,
-                               p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
+    rows_task<8, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
+                                   nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
 }
 
 // ---------------------------------------------------------------- D2: route + sort
 
+template <int PER>
 __global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
   __shared__ uint32_t idx_sh[64], sid_sh[64], key_sh[64], lds[4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int t = wave; t < p.T; t += 4) {
     uint32_t my_idx, my_score;
-    route_token(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score, lds[wave]);
+    route_token<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score, lds[wave]);
     if (lane < p.k) {
       p.idx[t * p.k + lane] = my_idx;
       p.scores[t * p.k + lane] = (uint16_t)my_score;
@@ -311,14 +323,15 @@ __global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
   // expert offsets [E+2] (E+1: trailing out-of-range bucket, empty here)
   for (int e = threadIdx.x; e <= p.E + 1; e += 256) {
     uint32_t c = 0;
-    for (int i = 0; i < A; ++i) c += sid_sh[i] < (uint32_t)e;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) c += (i < A) & (sid_sh[i] < (uint32_t)e);
     p.offsets[e] = e <= p.E ? c : (uint32_t)A;
   }
 }
 
 // ---------------------------------------------------------------- D3: routed gate/up
 
-template <int BITS, int MT>
+template <int BITS, int MT, int NC>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
   __shared__ int rows_sh[MT], orows_sh[MT];
   const int g = blockIdx.y;
@@ -326,10 +339,11 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
   if (g >= ng || g >= p.max_groups) return;
   const uint32_t e = p.g_expert[g], start = p.g_start[g], m = p.g_count[g];
   if (e >= (uint32_t)p.E || start + m > (uint32_t)p.A || m > (uint32_t)MT || m == 0) return;
-  if (threadIdx.x < m) {
-    const uint32_t tok = p.sorted_order[start + threadIdx.x] / (uint32_t)p.k;
+  if (threadIdx.x < MT) {
+    const uint32_t i = threadIdx.x < m ? threadIdx.x : m - 1;
+    const uint32_t tok = p.sorted_order[start + i] / (uint32_t)p.k;
     rows_sh[threadIdx.x] = (int)(tok < (uint32_t)p.T ? tok : 0u);
-    orows_sh[threadIdx.x] = (int)(start + threadIdx.x);
+    orows_sh[threadIdx.x] = (int)(start + i);
   }
   __syncthreads();
   const int wave = threadIdx.x >> 6;
@@ -338,111 +352,125 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
   const int nrows = min(4, p.I - r0);
   const int64_t wo = (int64_t)e * p.gu_w_es + (int64_t)r0 * p.gu_w_rs;
   const int64_t so = (int64_t)e * p.gu_sb_es + (int64_t)r0 * p.gu_sb_rs;
-  rows_task<BITS, MT, 4, true>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
-                               p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows, p.H,
-                               p.gu_group, p.x, p.H, rows_sh, (int)m, p.act + r0, p.act_ld,
-                               orows_sh);
+  rows_task<BITS, MT, 4, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
+                                   p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows,
+                                   p.H / 32, p.gu_group, p.x, p.H, rows_sh, (int)m,
+                                   p.act + r0, p.act_ld, orows_sh);
 }
 
 // ---------------------------------------------------------------- D4: down (routed + shared)
 
-// One wave per (group, 64 output rows).  Quarter q of the wave takes rows 4*it + q; its 16
-// lanes split the row's input chunks (lane l16 takes chunks l16, l16+16).
-template <int BITS, int MT>
+// One wave per (group, HR output rows).  Quarter q of the wave (one DPP row of 16 lanes)
+// takes rows 4*it + q; its 16 lanes split the row's input chunks (lane l16 takes chunks
+// l16, l16+16, ...).  Branch-free like rows_task.
+template <int BITS, int MT, int NC, int HR>
 __global__ __launch_bounds__(64) void decode_down_kernel(const DecodeArgs p) {
-  __shared__ uint16_t res[MT][64];
+  constexpr int IT = HR / 4;
+  __shared__ uint16_t res[MT][HR];
   const int lane = threadIdx.x, l16 = lane & 15, q = lane >> 4;
   const int g = blockIdx.y;
   const int ng = (int)*p.n_groups;
   const bool shared = p.Is > 0 && g == ng;
   if (g > ng || g > p.max_groups || (g == ng && !shared)) return;
-  int rows[MT], m, K, group;
+  int rows[MT], m, nchunks, group;
   const uint32_t *w;
   const uint16_t *sc, *bi;
   int64_t w_rs, sb_rs;
   if (shared) {
     m = p.T;
 #pragma unroll
-    for (int t = 0; t < MT; ++t) rows[t] = p.A + (t < m ? t : 0);
+    for (int t = 0; t < MT; ++t) rows[t] = p.A + (t < m ? t : m - 1);
     w = p.sd_w;
     sc = p.sd_s;
     bi = p.sd_b;
     w_rs = p.sd_w_rs;
     sb_rs = p.sd_sb_rs;
-    K = p.Is;
+    nchunks = p.Is / 32;
     group = p.sd_group;
   } else {
     const uint32_t e = p.g_expert[g], start = p.g_start[g];
     m = (int)p.g_count[g];
     if (e >= (uint32_t)p.E || start + (uint32_t)m > (uint32_t)p.A || m > MT || m <= 0) return;
 #pragma unroll
-    for (int t = 0; t < MT; ++t) rows[t] = (int)start + (t < m ? t : 0);
+    for (int t = 0; t < MT; ++t) rows[t] = (int)start + (t < m ? t : m - 1);
     w = p.down_w + (int64_t)e * p.dn_w_es;
     sc = p.down_s + (int64_t)e * p.dn_sb_es;
     bi = p.down_b + (int64_t)e * p.dn_sb_es;
     w_rs = p.dn_w_rs;
     sb_rs = p.dn_sb_rs;
-    K = p.I;
+    nchunks = p.I / 32;
     group = p.dn_group;
   }
-  const int h0 = blockIdx.x * 64;
-  const int nchunks = K / 32;
-  float acc[16][MT];
+  const int h0 = blockIdx.x * HR;
+  float acc[IT][MT];
 #pragma unroll
-  for (int it = 0; it < 16; ++it)
+  for (int it = 0; it < IT; ++it)
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[it][t] = 0.0f;
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
-    const int c = l16 + 16 * cc;
-    if (c >= nchunks) break;
-    WChunk wch[16];
+  for (int cc = 0; cc < NC; ++cc) {
+    const int craw = l16 + 16 * cc;
+    const bool cv = craw < nchunks;
+    const int c = cv ? craw : 0;
+    WChunk wch[IT];
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < IT; ++it) {
       const int h = h0 + 4 * it + q;
-      if (h < p.H) load_wchunk<BITS>(wch[it], w + (int64_t)h * w_rs, sc + (int64_t)h * sb_rs,
-                                     bi + (int64_t)h * sb_rs, c, group);
+      load_wchunk<BITS>(wch[it], w + (int64_t)h * w_rs, sc + (int64_t)h * sb_rs,
+                        bi + (int64_t)h * sb_rs, c, group);
     }
+    XChunk xa[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      if (t < m) {
-        XChunk xc;
-        load_xchunk<BITS>(xc, p.act + (int64_t)rows[t] * p.act_ld + c * 32);
+    for (int t = 0; t < MT; ++t) load_xchunk<BITS>(xa[t], p.act + (int64_t)rows[t] * p.act_ld + c * 32);
 #pragma unroll
-        for (int it = 0; it < 16; ++it)
-          if (h0 + 4 * it + q < p.H) acc[it][t] += chunk_dot<BITS>(wch[it], xc);
+    for (int it = 0; it < IT; ++it)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const float d = chunk_dot<BITS>(wch[it], xa[t]);
+        acc[it][t] += cv ? d : 0.0f;
       }
-    }
   }
 #pragma unroll
-  for (int it = 0; it < 16; ++it) {
+  for (int it = 0; it < IT; ++it)
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      if (t < m) {
-        const float v = row_sum(acc[it][t]);
-        if (l16 == 0) res[t][4 * it + q] = (uint16_t)f2bf(v);
-      }
+      const float v = row_sum(acc[it][t]);
+      if (l16 == 0) res[t][4 * it + q] = (uint16_t)f2bf(v);
     }
-  }
   __syncthreads();
-  const int h = h0 + lane;
-  if (h < p.H) {
+  if (lane < HR) {
+    const int h = h0 + lane;
 #pragma unroll
     for (int t = 0; t < MT; ++t)
       if (t < m) p.down_out[(int64_t)rows[t] * p.H + h] = res[t][lane];
   }
 }
 
+constexpr int down_rows(int mt) { return mt <= 2 ? 32 : 16; }
+
+template <int BITS, int MT, int NC>
+void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT, NC>), dim3((a.I + 15) / 16, a.max_groups),
+                     dim3(256), 0, s, a);
+}
+
+template <int BITS, int MT, int NC>
+void launch_down_nc(const DecodeArgs &a, hipStream_t s) {
+  constexpr int HR = down_rows(MT);
+  hipLaunchKernelGGL((decode_down_kernel<BITS, MT, NC, HR>),
+                     dim3(a.H / HR, a.max_groups + (a.Is > 0 ? 1 : 0)), dim3(64), 0, s, a);
+}
+
 template <int BITS, int MT>
 void launch_gate_up_mt(const DecodeArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT>), dim3((a.I + 15) / 16, a.max_groups),
-                     dim3(256), 0, s, a);
+  if (a.H <= 2048) launch_gate_up_nc<BITS, MT, 1>(a, s);
+  else launch_gate_up_nc<BITS, MT, 2>(a, s);
 }
 
 template <int BITS, int MT>
 void launch_down_mt(const DecodeArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((decode_down_kernel<BITS, MT>),
-                     dim3((a.H + 63) / 64, a.max_groups + (a.Is > 0 ? 1 : 0)), dim3(64), 0, s, a);
+  if (std::max(a.I, a.Is) <= 512) launch_down_nc<BITS, MT, 1>(a, s);
+  else launch_down_nc<BITS, MT, 2>(a, s);
 }
 
 template <int BITS>
@@ -461,15 +489,38 @@ void launch_down(const DecodeArgs &a, int mt, hipStream_t s) {
   else launch_down_mt<BITS, 8>(a, s);
 }
 
+template <int MT, int NC>
+void launch_router_nc(const DecodeArgs &a, int blocks, hipStream_t s) {
+  hipLaunchKernelGGL((decode_router_shared_kernel<MT, NC>), dim3(blocks), dim3(256), 0, s, a);
+}
+
+template <int MT>
+void launch_router(const DecodeArgs &a, int blocks, hipStream_t s) {
+  if (a.H <= 2048) launch_router_nc<MT, 1>(a, blocks, s);
+  else launch_router_nc<MT, 2>(a, blocks, s);
+}
+
+void launch_route(const DecodeArgs &a, hipStream_t s) {
+  const int per = (a.E + 63) / 64;
+  if (per <= 1) hipLaunchKernelGGL(decode_route_kernel<1>, dim3(1), dim3(256), 0, s, a);
+  else if (per <= 2) hipLaunchKernelGGL(decode_route_kernel<2>, dim3(1), dim3(256), 0, s, a);
+  else if (per <= 4) hipLaunchKernelGGL(decode_route_kernel<4>, dim3(1), dim3(256), 0, s, a);
+  else if (per <= 8) hipLaunchKernelGGL(decode_route_kernel<8>, dim3(1), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(decode_route_kernel<16>, dim3(1), dim3(256), 0, s, a);
+}
+
 }  // namespace
 
 bool decode_supported(const DecodeArgs &a) {
+  const int mt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8;
   return a.T >= 1 && a.T <= 8 && a.A <= 64 && a.router_w != nullptr && a.H % 32 == 0 &&
-         a.H <= 4096 && a.I % 32 == 0 && a.I <= 1024 && a.Is % 32 == 0 && a.Is <= 1024 &&
-         a.E <= 1024 && a.k <= 64 && (a.gu_bits == 4 || a.gu_bits == 8) &&
-         (a.dn_bits == 4 || a.dn_bits == 8) && a.gu_group >= 32 && a.dn_group >= 32 &&
+         a.H % down_rows(mt) == 0 && a.H <= 4096 && a.I % 32 == 0 && a.I <= 1024 &&
+         a.Is % 32 == 0 && a.Is <= 1024 && a.E <= 1024 && a.k <= 64 &&
+         (a.gu_bits == 4 || a.gu_bits == 8) && (a.dn_bits == 4 || a.dn_bits == 8) &&
+         a.gu_group >= 32 && a.dn_group >= 32 &&
          (a.Is == 0 || (a.sd_bits == a.dn_bits && (a.sg_bits == 4 || a.sg_bits == 8) &&
-                        (a.sz_bits == 4 || a.sz_bits == 8)));
+                        (a.sz_bits == 4 || a.sz_bits == 8) && a.sd_group >= 32 &&
+                        a.sg_group >= 32 && a.sz_group >= 32));
 }
 
 hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *marks) {
@@ -481,16 +532,14 @@ hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *m
   // D1: router rows (4 experts per block), shared gate/up (16 rows per block), output gate
   const int blocks = a.router_blocks + a.shared_pair_blocks + (a.sz_w ? 1 : 0);
   mark();
-  switch (mt) {
-    case 1: hipLaunchKernelGGL(decode_router_shared_kernel<1>, dim3(blocks), dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(decode_router_shared_kernel<2>, dim3(blocks), dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(decode_router_shared_kernel<4>, dim3(blocks), dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(decode_router_shared_kernel<8>, dim3(blocks), dim3(256), 0, s, a); break;
-  }
+  if (mt == 1) launch_router<1>(a, blocks, s);
+  else if (mt == 2) launch_router<2>(a, blocks, s);
+  else if (mt == 4) launch_router<4>(a, blocks, s);
+  else launch_router<8>(a, blocks, s);
   hipError_t e = hipGetLastError();
   mark();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(256), 0, s, a);
+  launch_route(a, s);
   e = hipGetLastError();
   mark();  // sorting happens inside the route kernel: the sort stage is empty here
   mark();

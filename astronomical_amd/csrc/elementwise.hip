@@ -8,6 +8,8 @@ namespace astro {
 
 namespace {
 
+constexpr int kHoistK = 16;  // top-k widths whose combine loads are all issued up front
+
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict__ g,
                                                      const uint16_t *__restrict__ u, int64_t n,
                                                      uint16_t *__restrict__ out) {
@@ -32,6 +34,31 @@ __global__ __launch_bounds__(256) void combine_kernel(
   if (gid >= (int64_t)T * chunks) return;
   const int t = (int)(gid / chunks), d0 = (int)(gid % chunks) * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (VEC && k >= 1 && k <= kHoistK) {
+    // every index, score and row load is issued before the first use; slots past k
+    // repeat the last slot and are masked out of the (ordered) accumulation
+    uint32_t inv[kHoistK];
+    float sc[kHoistK];
+#pragma unroll
+    for (int j = 0; j < kHoistK; ++j) {
+      const int64_t a = (int64_t)t * k + (j < k ? j : k - 1);
+      inv[j] = inverse_order ? inverse_order[a] : (uint32_t)a;
+      sc[j] = bf2f(scores[a]);
+    }
+    u32x4 q[kHoistK];
+#pragma unroll
+    for (int j = 0; j < kHoistK; ++j) q[j] = *(const u32x4 *)(rows + (int64_t)inv[j] * D + d0);
+#pragma unroll
+    for (int j = 0; j < kHoistK; ++j) {
+      const bool on = j < k;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = (i & 1) ? bf_hi(q[j][i >> 1]) : bf_lo(q[j][i >> 1]);
+        const float nxt = sorted ? __builtin_fmaf(v, sc[j], acc[i]) : acc[i] + round_bf(v * sc[j]);
+        acc[i] = on ? nxt : acc[i];
+      }
+    }
+  } else
   for (int j = 0; j < k; ++j) {
     const int64_t a = (int64_t)t * k + j;
     const int64_t r = inverse_order ? (int64_t)inverse_order[a] : a;

@@ -9,6 +9,7 @@ namespace astro {
 namespace {
 
 // One wave per token (route_token in route_dev.h).
+template <int PER>
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restrict__ logits,
                                                          int T, int E, int k, int normalize,
                                                          uint32_t *__restrict__ idx,
@@ -18,7 +19,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restr
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
   uint32_t my_idx, my_score;
-  route_token(logits + (int64_t)t * E, E, k, normalize, my_idx, my_score, lds[wave]);
+  route_token<PER>(logits + (int64_t)t * E, E, k, normalize, my_idx, my_score, lds[wave]);
   if (lane < k) {
     idx[(int64_t)t * k + lane] = my_idx;
     scores[(int64_t)t * k + lane] = (uint16_t)my_score;
@@ -127,8 +128,18 @@ __global__ __launch_bounds__(kScatterThreads) void sort_scatter_kernel(
 hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
                              uint32_t *idx, uint16_t *scores, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(route_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, k,
-                     normalize, idx, scores);
+  const dim3 grid((T + 3) / 4), block(256);
+  const int per = (E + 63) / 64;
+  if (per <= 1)
+    hipLaunchKernelGGL(route_topk_kernel<1>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+  else if (per <= 2)
+    hipLaunchKernelGGL(route_topk_kernel<2>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+  else if (per <= 4)
+    hipLaunchKernelGGL(route_topk_kernel<4>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+  else if (per <= 8)
+    hipLaunchKernelGGL(route_topk_kernel<8>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+  else
+    hipLaunchKernelGGL(route_topk_kernel<16>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
   return hipGetLastError();
 }
 

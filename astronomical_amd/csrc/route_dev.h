@@ -6,8 +6,6 @@
 
 namespace astro {
 
-constexpr int kRouteMaxPerLane = 16;  // experts per lane: E <= 1024
-
 // Lane j holds experts j, j+64, ...; softmax denominator = each lane's sequential sum,
 // then the 64-lane tree (wave_sum); p = bf16(e * (1/S)).
 //
@@ -17,35 +15,36 @@ constexpr int kRouteMaxPerLane = 16;  // experts per lane: E <= 1024
 // bits with wave ballots; the k selected keys are compacted through `lds` (64 words per
 // wave), ranked, and permuted so that lane j < k holds slot j of the ascending slice.
 // Lane j < k returns slot j's expert and (renormalised) score as bf16 bits.
+// PER = experts per lane (ceil(E / 64), E <= 64 * PER).
+template <int PER>
 __device__ __forceinline__ void route_token(const uint16_t *__restrict__ l, int E, int k,
                                             int normalize, uint32_t &out_idx,
                                             uint32_t &out_score, uint32_t *lds) {
 #pragma clang fp contract(off)
   const int lane = (int)(threadIdx.x & 63);
-  const int per = (E + 63) >> 6;
-  float v[kRouteMaxPerLane];
+  float v[PER];
   float m = -__builtin_inff();
 #pragma unroll
-  for (int i = 0; i < kRouteMaxPerLane; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int e = lane + 64 * i;
-    v[i] = (i < per && e < E) ? bf2f(l[e]) : -__builtin_inff();
+    v[i] = (e < E) ? bf2f(l[e]) : -__builtin_inff();
     m = fmaxf(m, v[i]);
   }
   m = wave_max_fast(m);
   float part = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kRouteMaxPerLane; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int e = lane + 64 * i;
-    v[i] = (i < per && e < E) ? det_expf(v[i] - m) : 0.0f;
+    v[i] = (e < E) ? det_expf(v[i] - m) : 0.0f;
     part = part + v[i];
   }
   const float rcp = 1.0f / wave_sum(part);
-  uint32_t cand[kRouteMaxPerLane];
+  uint32_t cand[PER];
 #pragma unroll
-  for (int i = 0; i < kRouteMaxPerLane; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int e = lane + 64 * i;
     // key + 1, so that 0 marks an empty entry
-    cand[i] = (i < per && e < E) ? (((f2bf(v[i] * rcp) << 16) | (uint32_t)e) + 1u) : 0u;
+    cand[i] = (e < E) ? (((f2bf(v[i] * rcp) << 16) | (uint32_t)e) + 1u) : 0u;
   }
   // radix select: thr = the k-th largest candidate (keys are distinct, so exactly k
   // candidates are >= thr); candidates stay below 2^30
@@ -54,21 +53,19 @@ __device__ __forceinline__ void route_token(const uint16_t *__restrict__ l, int 
     const uint32_t c = thr | (1u << bit);
     int cnt = 0;
 #pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; ++i)
-      if (i < per) cnt += __popcll(__ballot(cand[i] >= c));
+    for (int i = 0; i < PER; ++i)
+      cnt += __popcll(__ballot(cand[i] >= c));
     if (cnt >= k) thr = c;
   }
   // compact the selected keys into lds[0..k)
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   int base = 0;
 #pragma unroll
-  for (int i = 0; i < kRouteMaxPerLane; ++i) {
-    if (i < per) {
-      const bool sel = cand[i] >= thr;
-      const uint64_t mask = __ballot(sel);
-      if (sel) lds[base + __popcll(mask & below)] = cand[i] - 1u;
-      base += __popcll(mask);
-    }
+  for (int i = 0; i < PER; ++i) {
+    const bool sel = cand[i] >= thr;
+    const uint64_t mask = __ballot(sel);
+    if (sel) lds[base + __popcll(mask & below)] = cand[i] - 1u;
+    base += __popcll(mask);
   }
   __builtin_amdgcn_wave_barrier();
   // rank among the selected keys, then send each key to the lane of its rank
