@@ -407,7 +407,7 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     d.down_out = eout;
     d.z = z;
     d.router_blocks = (E + 3) / 4;
-    d.shared_pair_blocks = has_shared ? (d.Is + 15) / 16 : 0;
+    d.shared_pair_blocks = has_shared ? (d.Is + 4 * kDecodeRowsPerWave - 1) / (4 * kDecodeRowsPerWave) : 0;
     d.max_groups = std::min(A, E);
     if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
     hipError_t e = launch_decode_block(d, s, marks);

@@ -72,13 +72,28 @@ __device__ __forceinline__ uint32_t swiglu_bf(float g, float u) {
   return f2bf(a * u);
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the total.  The butterfly adds
-// lane j and lane j^off for off = 32, 16, ..., 1, i.e. the binary tree
-// lane[j] += lane[j + off] evaluated at lane 0.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Canonical sum over the 64 lanes of a wave (the softmax denominator; the host oracle
+// reproduces it bit for bit): the butterfly new[j] = v[j] + v[j ^ off] for
+// off = 1, 2, 4, 8, 16, 32, value of lane 0.  Offsets 1 and 2 are DPP quad permutes; after
+// them values are uniform within quads, so the half-row and row mirrors pair the same
+// partial sums as offsets 4 and 8; the last two levels add the four row sums as
+// (row0 + row1) + (row2 + row3).  Returns the sum in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma clang fp contract(off)
-  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
-  return v;
+  v = v + dpp_f32<0xb1>(v);   // quad_perm [1,0,3,2]: lane j ^ 1
+  v = v + dpp_f32<0x4e>(v);   // quad_perm [2,3,0,1]: lane j ^ 2
+  v = v + dpp_f32<0x141>(v);  // row_half_mirror: the other quad of the 8-lane half
+  v = v + dpp_f32<0x140>(v);  // row_mirror: the other half of the 16-lane row
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
@@ -126,6 +141,19 @@ __device__ __forceinline__ float wave_sum_fast(float v) {
   const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
   const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
   return (r0 + r1) + (r2 + r3);
+}
+
+// Maximum over the wave of unsigned keys; uniform result.
+__device__ __forceinline__ uint32_t wave_max_u32_fast(uint32_t v) {
+  v = max(v, row_ror_u32<8>(v));
+  v = max(v, row_ror_u32<4>(v));
+  v = max(v, row_ror_u32<2>(v));
+  v = max(v, row_ror_u32<1>(v));
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(r0, r1), max(r2, r3));
 }
 
 __device__ __forceinline__ float wave_max_fast(float v) {

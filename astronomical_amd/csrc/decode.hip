@@ -25,6 +25,10 @@ namespace {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
+// (gate row, up row) pairs per wave in the gate/up GEMVs: one keeps each wave's serial
+// instruction chain short; the chip has wave slots to spare at decode sizes
+constexpr int kRowsPerWave = kDecodeRowsPerWave;
+
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
                                          c, false);
@@ -245,17 +249,17 @@ __global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeA
   const int sb = b - p.router_blocks;
   if (sb < p.shared_pair_blocks) {
     // shared expert gate/up + SwiGLU: rows 16*sb .. of [Is], 4 per wave
-    const int r0 = (sb * 4 + wave) * 4;
+    const int r0 = (sb * 4 + wave) * kRowsPerWave;
     if (r0 >= p.Is) return;
-    const int nrows = min(4, p.Is - r0);
+    const int nrows = min(kRowsPerWave, p.Is - r0);
     if (p.sg_bits == 4)
-      rows_task<4, MT, 4, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
+      rows_task<4, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
                                     p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
                                     p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs, p.sg_w_rs,
                                     p.sg_sb_rs, nrows, nchunks, p.sg_group, p.x, p.H, rows_sh, p.T,
                                     p.act + r0, p.act_ld, orows_sh);
     else
-      rows_task<8, MT, 4, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
+      rows_task<8, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
                                     p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
                                     p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs, p.sg_w_rs,
                                     p.sg_sb_rs, nrows, nchunks, p.sg_group, p.x, p.H, rows_sh, p.T,
@@ -276,11 +280,11 @@ __global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeA
 
 template <int PER>
 __global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
-  __shared__ uint32_t idx_sh[64], sid_sh[64], key_sh[64], lds[4][64];
+  __shared__ uint32_t idx_sh[64], sid_sh[64], key_sh[64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int t = wave; t < p.T; t += 4) {
     uint32_t my_idx, my_score;
-    route_token<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score, lds[wave]);
+    route_token<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score);
     if (lane < p.k) {
       p.idx[t * p.k + lane] = my_idx;
       p.scores[t * p.k + lane] = (uint16_t)my_score;
@@ -347,12 +351,12 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
   }
   __syncthreads();
   const int wave = threadIdx.x >> 6;
-  const int r0 = (blockIdx.x * 4 + wave) * 4;
+  const int r0 = (blockIdx.x * 4 + wave) * kRowsPerWave;
   if (r0 >= p.I) return;
-  const int nrows = min(4, p.I - r0);
+  const int nrows = min(kRowsPerWave, p.I - r0);
   const int64_t wo = (int64_t)e * p.gu_w_es + (int64_t)r0 * p.gu_w_rs;
   const int64_t so = (int64_t)e * p.gu_sb_es + (int64_t)r0 * p.gu_sb_rs;
-  rows_task<BITS, MT, 4, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
+  rows_task<BITS, MT, kRowsPerWave, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
                                    p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows,
                                    p.H / 32, p.gu_group, p.x, p.H, rows_sh, (int)m,
                                    p.act + r0, p.act_ld, orows_sh);
@@ -446,11 +450,11 @@ __global__ __launch_bounds__(64) void decode_down_kernel(const DecodeArgs p) {
   }
 }
 
-constexpr int down_rows(int mt) { return mt <= 2 ? 32 : 16; }
+constexpr int down_rows(int mt) { return mt <= 2 ? 16 : 8; }
 
 template <int BITS, int MT, int NC>
 void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT, NC>), dim3((a.I + 15) / 16, a.max_groups),
+  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT, NC>), dim3((a.I + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave), a.max_groups),
                      dim3(256), 0, s, a);
 }
 

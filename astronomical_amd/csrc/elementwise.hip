@@ -8,8 +8,6 @@ namespace astro {
 
 namespace {
 
-constexpr int kHoistK = 16;  // top-k widths whose combine loads are all issued up front
-
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict__ g,
                                                      const uint16_t *__restrict__ u, int64_t n,
                                                      uint16_t *__restrict__ out) {
@@ -17,15 +15,37 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict_
   if (i < n) out[i] = (uint16_t)swiglu_bf(bf2f(g[i]), bf2f(u[i]));
 }
 
+// Accumulate one expert row into the 8 running sums: sorted rounding (fp32 fma of
+// out*score, weighted_sum.rs:16-33) or unsorted rounding (bf16 product, then fp32 add,
+// weighted_sum.rs:112-119).
+template <bool SORTED>
+__device__ __forceinline__ void accumulate8(float acc[8], const float v[8], float s) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (SORTED) acc[i] = __builtin_fmaf(v[i], s, acc[i]);
+    else acc[i] = acc[i] + round_bf(v[i] * s);
+  }
+}
+
+__device__ __forceinline__ void unpack8(float v[8], const u32x4 q) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf_lo(q[i]);
+    v[2 * i + 1] = bf_hi(q[i]);
+  }
+}
+
 // y[t][d] for 8 consecutive d per thread.  Row of assignment (t, j): inverse_order[t*k+j]
-// (or t*k+j when inverse_order is null).  sorted: fp32 fma accumulation of out*score in
-// slot order, one bf16 rounding (weighted_sum.rs:16-33).  unsorted: bf16 product per
-// slot, fp32 accumulation, one bf16 rounding (weighted_sum.rs:112-119).  Then, with a
-// shared expert: y = bf16(sparse + bf16(shared * bf16(sigmoid(z)))) (output_combination.rs:40-42).
-template <bool VEC>
+// (or t*k+j when inverse_order is null); slots are summed in slot order with one bf16
+// rounding at the end.  Then, with a shared expert:
+// y = bf16(sparse + bf16(shared * bf16(sigmoid(z)))) (output_combination.rs:40-42).
+// K > 0: the top-k width is K and every index, score and row load is issued before the
+// first use; K == 0: any k, element loads (no alignment or width assumptions).
+template <bool SORTED, int K>
 __global__ __launch_bounds__(256) void combine_kernel(
     const uint16_t *__restrict__ rows, const uint32_t *__restrict__ inverse_order,
-    const uint16_t *__restrict__ scores, int T, int k, int D, int sorted,
+    const uint16_t *__restrict__ scores, int T, int k, int D,
     const uint16_t *__restrict__ shared_out, const uint16_t *__restrict__ gate_logits,
     uint16_t *__restrict__ sparse_out, uint16_t *__restrict__ y) {
 #pragma clang fp contract(off)
@@ -34,73 +54,64 @@ __global__ __launch_bounds__(256) void combine_kernel(
   if (gid >= (int64_t)T * chunks) return;
   const int t = (int)(gid / chunks), d0 = (int)(gid % chunks) * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (VEC && k >= 1 && k <= kHoistK) {
-    // every index, score and row load is issued before the first use; slots past k
-    // repeat the last slot and are masked out of the (ordered) accumulation
-    uint32_t inv[kHoistK];
-    float sc[kHoistK];
+  if (K > 0) {
+    uint32_t inv[K > 0 ? K : 1];
+    float sc[K > 0 ? K : 1];
 #pragma unroll
-    for (int j = 0; j < kHoistK; ++j) {
-      const int64_t a = (int64_t)t * k + (j < k ? j : k - 1);
+    for (int j = 0; j < K; ++j) {
+      const int64_t a = (int64_t)t * K + j;
       inv[j] = inverse_order ? inverse_order[a] : (uint32_t)a;
       sc[j] = bf2f(scores[a]);
     }
-    u32x4 q[kHoistK];
+    u32x4 q[K > 0 ? K : 1];
 #pragma unroll
-    for (int j = 0; j < kHoistK; ++j) q[j] = *(const u32x4 *)(rows + (int64_t)inv[j] * D + d0);
+    for (int j = 0; j < K; ++j) q[j] = *(const u32x4 *)(rows + (int64_t)inv[j] * D + d0);
 #pragma unroll
-    for (int j = 0; j < kHoistK; ++j) {
-      const bool on = j < k;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float v = (i & 1) ? bf_hi(q[j][i >> 1]) : bf_lo(q[j][i >> 1]);
-        const float nxt = sorted ? __builtin_fmaf(v, sc[j], acc[i]) : acc[i] + round_bf(v * sc[j]);
-        acc[i] = on ? nxt : acc[i];
-      }
+    for (int j = 0; j < K; ++j) {
+      float v[8];
+      unpack8(v, q[j]);
+      accumulate8<SORTED>(acc, v, sc[j]);
     }
-  } else
-  for (int j = 0; j < k; ++j) {
-    const int64_t a = (int64_t)t * k + j;
-    const int64_t r = inverse_order ? (int64_t)inverse_order[a] : a;
-    const float s = bf2f(scores[a]);
-    const uint16_t *src = rows + r * D + d0;
-    float v[8];
-    if (VEC) {
-      const u32x4 q = *(const u32x4 *)src;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = bf_lo(q[i]);
-        v[2 * i + 1] = bf_hi(q[i]);
-      }
-    } else {
+  } else {
+    for (int j = 0; j < k; ++j) {
+      const int64_t a = (int64_t)t * k + j;
+      const int64_t r = inverse_order ? (int64_t)inverse_order[a] : a;
+      const uint16_t *src = rows + r * D + d0;
+      float v[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = d0 + i < D ? bf2f(src[i]) : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (sorted) acc[i] = __builtin_fmaf(v[i], s, acc[i]);
-      else acc[i] = acc[i] + round_bf(v[i] * s);
+      accumulate8<SORTED>(acc, v, bf2f(scores[a]));
     }
   }
   uint32_t outb[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) outb[i] = f2bf(acc[i]);
+  const bool full = d0 + 8 <= D;
   if (sparse_out) {
     uint16_t *dst = sparse_out + (int64_t)t * D + d0;
-    for (int i = 0; i < 8; ++i)
-      if (d0 + i < D) dst[i] = (uint16_t)outb[i];
+    if (K > 0) {
+      *(u32x4 *)dst = u32x4{outb[0] | (outb[1] << 16), outb[2] | (outb[3] << 16),
+                            outb[4] | (outb[5] << 16), outb[6] | (outb[7] << 16)};
+    } else {
+      for (int i = 0; i < 8; ++i)
+        if (d0 + i < D) dst[i] = (uint16_t)outb[i];
+    }
   }
   if (shared_out) {
     const float gate = round_bf(det_sigmoid(bf2f(gate_logits[t])));
     const uint16_t *so = shared_out + (int64_t)t * D + d0;
+    float sv[8];
+    if (K > 0) {
+      unpack8(sv, *(const u32x4 *)so);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float sv = (VEC || d0 + i < D) ? bf2f(so[i]) : 0.f;
-      outb[i] = f2bf(bf2f(outb[i]) + round_bf(sv * gate));
+      for (int i = 0; i < 8; ++i) sv[i] = d0 + i < D ? bf2f(so[i]) : 0.f;
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) outb[i] = f2bf(bf2f(outb[i]) + round_bf(sv[i] * gate));
   }
   uint16_t *dst = y + (int64_t)t * D + d0;
-  if (VEC) {
+  if (K > 0 && full) {
     *(u32x4 *)dst = u32x4{outb[0] | (outb[1] << 16), outb[2] | (outb[3] << 16),
                           outb[4] | (outb[5] << 16), outb[6] | (outb[7] << 16)};
   } else {
@@ -121,7 +132,7 @@ __global__ __launch_bounds__(256) void combine_shared_kernel(
 }
 
 // One wave per (token, output row): lane l covers inputs 32l.. of each 2048-wide chunk,
-// dequantising in fp32 (scale*q + bias) and accumulating x*w with fma; wave tree sum.
+// dequantising in fp32 (scale*q + bias) and accumulating x*w with fma; wave sum.
 template <int BITS>
 __global__ __launch_bounds__(256) void qgemv_rows_kernel(
     const uint16_t *__restrict__ x, int T, int K, const uint32_t *__restrict__ w,
@@ -162,6 +173,32 @@ __global__ __launch_bounds__(256) void qgemv_rows_kernel(
   if (lane == 0) out[(int64_t)t * N + n] = (uint16_t)f2bf(acc);
 }
 
+template <bool SORTED, int K>
+void launch_combine_t(const uint16_t *rows, const uint32_t *inverse_order, const uint16_t *scores,
+                      int T, int k, int D, const uint16_t *shared_out, const uint16_t *gate_logits,
+                      uint16_t *sparse_out, uint16_t *y, hipStream_t s) {
+  const int64_t threads = (int64_t)T * ((D + 7) / 8);
+  hipLaunchKernelGGL((combine_kernel<SORTED, K>), dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                     0, s, rows, inverse_order, scores, T, k, D, shared_out, gate_logits,
+                     sparse_out, y);
+}
+
+template <bool SORTED>
+void launch_combine_s(const uint16_t *rows, const uint32_t *inverse_order, const uint16_t *scores,
+                      int T, int k, int D, const uint16_t *shared_out, const uint16_t *gate_logits,
+                      uint16_t *sparse_out, uint16_t *y, hipStream_t s) {
+  // the unrolled variants need 16-byte aligned rows of a width divisible by 8
+  const bool vec = (D % 8) == 0 && ((uintptr_t)rows % 16) == 0 && ((uintptr_t)y % 16) == 0 &&
+                   (!sparse_out || ((uintptr_t)sparse_out % 16) == 0) &&
+                   (!shared_out || ((uintptr_t)shared_out % 16) == 0);
+  if (vec && k == 8)
+    launch_combine_t<SORTED, 8>(rows, inverse_order, scores, T, k, D, shared_out, gate_logits, sparse_out, y, s);
+  else if (vec && k == 4)
+    launch_combine_t<SORTED, 4>(rows, inverse_order, scores, T, k, D, shared_out, gate_logits, sparse_out, y, s);
+  else
+    launch_combine_t<SORTED, 0>(rows, inverse_order, scores, T, k, D, shared_out, gate_logits, sparse_out, y, s);
+}
+
 }  // namespace
 
 hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *out,
@@ -175,16 +212,11 @@ hipError_t launch_combine(const uint16_t *rows, const uint32_t *inverse_order,
                           const uint16_t *scores, int T, int k, int D, int sorted,
                           const uint16_t *shared_out, const uint16_t *gate_logits,
                           uint16_t *sparse_out, uint16_t *y, hipStream_t s) {
-  const int64_t threads = (int64_t)T * ((D + 7) / 8);
-  if (threads <= 0) return hipSuccess;
-  const dim3 grid((unsigned)((threads + 255) / 256));
-  const bool vec = (D % 8) == 0 && ((uintptr_t)rows % 16) == 0 && ((uintptr_t)y % 16) == 0;
-  if (vec)
-    hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, s, rows, inverse_order, scores,
-                       T, k, D, sorted, shared_out, gate_logits, sparse_out, y);
+  if ((int64_t)T * ((D + 7) / 8) <= 0) return hipSuccess;
+  if (sorted)
+    launch_combine_s<true>(rows, inverse_order, scores, T, k, D, shared_out, gate_logits, sparse_out, y, s);
   else
-    hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, s, rows, inverse_order, scores,
-                       T, k, D, sorted, shared_out, gate_logits, sparse_out, y);
+    launch_combine_s<false>(rows, inverse_order, scores, T, k, D, shared_out, gate_logits, sparse_out, y, s);
   return hipGetLastError();
 }
 

@@ -106,6 +106,7 @@ struct DecodeArgs {
 };
 
 bool decode_supported(const DecodeArgs &a);
+constexpr int kDecodeRowsPerWave = 1;  // must match kRowsPerWave in decode.hip
 // launches the four decode kernels; marks (nullable) receives 6 stage boundaries
 hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *marks);
 

@@ -14,12 +14,11 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restr
                                                          int T, int E, int k, int normalize,
                                                          uint32_t *__restrict__ idx,
                                                          uint16_t *__restrict__ scores) {
-  __shared__ uint32_t lds[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
   uint32_t my_idx, my_score;
-  route_token<PER>(logits + (int64_t)t * E, E, k, normalize, my_idx, my_score, lds[wave]);
+  route_token<PER>(logits + (int64_t)t * E, E, k, normalize, my_idx, my_score);
   if (lane < k) {
     idx[(int64_t)t * k + lane] = my_idx;
     scores[(int64_t)t * k + lane] = (uint16_t)my_score;

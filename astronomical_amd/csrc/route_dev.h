@@ -11,15 +11,14 @@ namespace astro {
 //
 // Top-k keys are (bf16(p) << 16 | expert): a larger key is a larger probability with
 // ties broken toward the higher expert index, as MLX's (value, index) partition
-// comparator orders them.  The k-th largest key is found by a radix select over the key
-// bits with wave ballots; the k selected keys are compacted through `lds` (64 words per
-// wave), ranked, and permuted so that lane j < k holds slot j of the ascending slice.
-// Lane j < k returns slot j's expert and (renormalised) score as bf16 bits.
+// comparator orders them.  k rounds of a wave-wide maximum (DPP) take the keys in
+// descending order; lane j < k keeps slot j of the ascending slice and returns its
+// expert and (renormalised) score as bf16 bits.
 // PER = experts per lane (ceil(E / 64), E <= 64 * PER).
 template <int PER>
 __device__ __forceinline__ void route_token(const uint16_t *__restrict__ l, int E, int k,
                                             int normalize, uint32_t &out_idx,
-                                            uint32_t &out_score, uint32_t *lds) {
+                                            uint32_t &out_score) {
 #pragma clang fp contract(off)
   const int lane = (int)(threadIdx.x & 63);
   float v[PER];
@@ -46,46 +45,27 @@ __device__ __forceinline__ void route_token(const uint16_t *__restrict__ l, int 
     // key + 1, so that 0 marks an empty entry
     cand[i] = (e < E) ? (((f2bf(v[i] * rcp) << 16) | (uint32_t)e) + 1u) : 0u;
   }
-  // radix select: thr = the k-th largest candidate (keys are distinct, so exactly k
-  // candidates are >= thr); candidates stay below 2^30
-  uint32_t thr = 0;
-  for (int bit = 29; bit >= 0; --bit) {
-    const uint32_t c = thr | (1u << bit);
-    int cnt = 0;
+  // k rounds of a wave-wide maximum; round r fills slot k-1-r (ascending slice)
+  uint32_t my_key = 0;
+  for (int r = 0; r < k; ++r) {
+    uint32_t best = 0;
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
-      cnt += __popcll(__ballot(cand[i] >= c));
-    if (cnt >= k) thr = c;
-  }
-  // compact the selected keys into lds[0..k)
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  int base = 0;
+    for (int i = 0; i < PER; ++i) best = max(best, cand[i]);
+    const uint32_t top = wave_max_u32_fast(best);
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const bool sel = cand[i] >= thr;
-    const uint64_t mask = __ballot(sel);
-    if (sel) lds[base + __popcll(mask & below)] = cand[i] - 1u;
-    base += __popcll(mask);
+    for (int i = 0; i < PER; ++i) cand[i] = cand[i] == top ? 0u : cand[i];
+    my_key = lane == k - 1 - r ? top - 1u : my_key;
   }
-  __builtin_amdgcn_wave_barrier();
-  // rank among the selected keys, then send each key to the lane of its rank
-  const uint32_t key = lane < k ? lds[lane] : 0u;
-  uint32_t rank = (uint32_t)lane;
-  if (lane < k) {
-    rank = 0;
-    for (int j = 0; j < k; ++j) rank += lds[j] < key;
-  }
-  const uint32_t sorted_key = (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4), (int)key);
-  __builtin_amdgcn_wave_barrier();
-  const uint32_t my_idx = sorted_key & 0xffffu;
+  const uint32_t sorted_key = my_key;
   float s = bf2f(sorted_key >> 16);
   if (normalize) {
     // sum over the slice in slot order
     float sum = 0.0f;
-    for (int j = 0; j < k; ++j) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), j));
+    for (int j = 0; j < k; ++j)
+      sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), j));
     s = s / round_bf(sum);
   }
-  out_idx = my_idx;
+  out_idx = sorted_key & 0xffffu;
   out_score = f2bf(s);
 }
 

@@ -128,7 +128,8 @@ void orc_router_logits(const uint16_t *x, const uint16_t *w, int32_t T, int32_t 
  * Softmax: m = max; e_i = exp(l_i - m); S = sum e_i; p_i = bf16(e_i * (1/S)) (MLX's
  * CPU softmax multiplies by the reciprocal of the normaliser).  The order of the
  * sum is canonical: lane j of 64 sums i = j, j+64, ... in order, then the 64 lane
- * sums are added as a binary tree (lane j += lane j+off for off = 32..1).
+ * sums are combined by the butterfly lane[j] = lane[j] + lane[j ^ off] for
+ * off = 1, 2, 4, 8, 16, 32 and S is lane 0.
  *
  * Selection: MLX's partition comparator orders (value, index) with index as the tie
  * break, so the selected set is the k largest (p, index) pairs — a tie at the
@@ -165,8 +166,11 @@ int orc_route_topk(const uint16_t *logits, int32_t T, int32_t E, int32_t k,
         }
         for (int j = 0; j < ORC_LANES; ++j)
           for (int32_t i = j; i < E; i += ORC_LANES) lane[j] = lane[j] + ex[i];
-        for (int off = ORC_LANES / 2; off >= 1; off >>= 1)
-          for (int j = 0; j < off; ++j) lane[j] = lane[j] + lane[j + off];
+        for (int off = 1; off < ORC_LANES; off <<= 1) {
+          float next[ORC_LANES];
+          for (int j = 0; j < ORC_LANES; ++j) next[j] = lane[j] + lane[j ^ off];
+          for (int j = 0; j < ORC_LANES; ++j) lane[j] = next[j];
+        }
         const float rcp = 1.0f / lane[0];
         for (int32_t i = 0; i < E; ++i) {
           pb[i] = tobf(ex[i] * rcp);
