@@ -117,14 +117,12 @@ struct Layout {
 // and shapes its per-lane register tiles cover (decode.hip: decode_supported).
 bool decode_path(const astro_moe_layer &L, int T) {
   const int Is = L.shared_intermediate > 0 ? L.shared_intermediate : 0;
-  const int mt = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8;
   const astro_moe_affine &gu = L.gate_up.w ? L.gate_up : L.gate;
-  return T >= 1 && T <= 8 && T * L.top_k <= 64 && L.router_w != nullptr && L.hidden <= 4096 &&
+  return T >= 1 && T <= 8 && T * L.top_k <= 64 && L.top_k <= kDecodeMaxK &&
+         L.router_w != nullptr && L.hidden <= 4096 &&
          L.intermediate <= 1024 && Is <= 1024 && (gu.bits == 4 || gu.bits == 8) &&
          (L.down.bits == 4 || L.down.bits == 8) &&
-         (Is == 0 || L.shared_down.bits == L.down.bits) &&
-         // the down kernel keeps every token's activation chunks in registers
-         (L.intermediate <= 512 || mt <= 4);
+         (Is == 0 || L.shared_down.bits == L.down.bits);
 }
 
 Layout block_layout(const astro_moe_layer &L, int T) {
@@ -406,15 +404,17 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     d.act_ld = o.act_ld;
     d.down_out = eout;
     d.z = z;
+    d.sparse = sparse;
+    d.y = y;
     d.router_blocks = (E + 3) / 4;
     d.shared_pair_blocks = has_shared ? (d.Is + 4 * kDecodeRowsPerWave - 1) / (4 * kDecodeRowsPerWave) : 0;
     d.max_groups = std::min(A, E);
     if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
     hipError_t e = launch_decode_block(d, s, marks);
     stage = 6;  // launch_decode_block recorded marks[0..5]
-    mark();     // the shared expert ran inside the router and down kernels: empty stage
-    if (e == hipSuccess)
-      e = launch_combine(eout, inverse, scores, T, k, H, A >= 64, shared_out, z, sparse, y, s);
+    // the shared expert ran inside the router and down kernels, the combine inside the
+    // down kernel: empty stages
+    mark();
     mark();
     if (e != hipSuccess) return hip_fail(kBlockOp, e);
     return ok();

@@ -72,6 +72,26 @@ __device__ __forceinline__ uint32_t swiglu_bf(float g, float u) {
   return f2bf(a * u);
 }
 
+// One output element of the weighted combine (weighted_sum.rs:16-33 sorted / :112-119
+// unsorted) followed by the shared expert's gated add (output_combination.rs:40-42):
+// v[j] = expert row values of the token's k slots (slot order), s[j] = their scores.
+template <bool SORTED, int KMAX>
+__device__ __forceinline__ uint32_t combine_element(const float *v, const float *s, int k) {
+#pragma clang fp contract(off)
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    const float nxt = SORTED ? __builtin_fmaf(v[j], s[j], acc) : acc + round_bf(v[j] * s[j]);
+    acc = j < k ? nxt : acc;
+  }
+  return f2bf(acc);
+}
+__device__ __forceinline__ uint32_t shared_gated_add(uint32_t sparse_bits, float shared_value,
+                                                     float gate_bf) {
+#pragma clang fp contract(off)
+  return f2bf(bf2f(sparse_bits) + round_bf(shared_value * gate_bf));
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));

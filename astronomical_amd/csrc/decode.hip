@@ -1,14 +1,12 @@
 // Decode path of the block (T <= 8 tokens, T*k <= 64 assignments): wavefront GEMVs
-// instead of MFMA tiles.  Per layer:
+// instead of MFMA tiles, three kernels per layer:
 //   D1  router GEMV (one wave per expert row) + the shared expert's gate/up + SwiGLU and
 //       its output gate — all the work that does not depend on routing;
-//   D2  route: softmax/top-k per token, the sort of the <= 64 assignments and the table of
-//       distinct experts (one workgroup);
-//   D3  routed gate/up GEMV + SwiGLU: one wave per 4 (gate row, up row) pairs of one
-//       selected expert, every token routed to it;
-//   D4  down GEMV for the routed experts and the shared expert (16 lanes per row, 64 rows
-//       per wave);
-//   then the weighted combine (launch_combine).
+//   D2  routing (softmax/top-k, the sort of the assignments, the distinct-expert table),
+//       recomputed by every workgroup, then the routed gate/up GEMV + SwiGLU: one wave
+//       per (gate row, up row) pair of one selected expert, every token routed to it;
+//   D3  per token: down GEMV rows of its k experts and of the shared expert (16 lanes per
+//       row), then the weighted combine and the shared expert's gated add in registers.
 // Affine rows are read once per distinct expert with 16 B per lane loads.  4-bit codes are
 // turned into bf16 pairs (128 + q) with one and/or per pair and multiplied by
 // v_dot2_f32_bf16; the per-group affine terms are applied per 32-input chunk:
@@ -248,22 +246,24 @@ __global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeA
   }
   const int sb = b - p.router_blocks;
   if (sb < p.shared_pair_blocks) {
-    // shared expert gate/up + SwiGLU: rows 16*sb .. of [Is], 4 per wave
+    // shared expert gate/up + SwiGLU
     const int r0 = (sb * 4 + wave) * kRowsPerWave;
     if (r0 >= p.Is) return;
     const int nrows = min(kRowsPerWave, p.Is - r0);
     if (p.sg_bits == 4)
       rows_task<4, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
-                                    p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
-                                    p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs, p.sg_w_rs,
-                                    p.sg_sb_rs, nrows, nchunks, p.sg_group, p.x, p.H, rows_sh, p.T,
-                                    p.act + r0, p.act_ld, orows_sh);
+                                               p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
+                                               p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
+                                               p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
+                                               p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
+                                               orows_sh);
     else
       rows_task<8, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
-                                    p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
-                                    p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs, p.sg_w_rs,
-                                    p.sg_sb_rs, nrows, nchunks, p.sg_group, p.x, p.H, rows_sh, p.T,
-                                    p.act + r0, p.act_ld, orows_sh);
+                                               p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
+                                               p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
+                                               p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
+                                               p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
+                                               orows_sh);
     return;
   }
   // the shared expert's output gate (one row) -> z[t]
@@ -276,25 +276,33 @@ __global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeA
                                    nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
 }
 
-// ---------------------------------------------------------------- D2: route + sort
+// ---------------------------------------------------------------- D2: route + routed gate/up
 
-template <int PER>
-__global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
-  __shared__ uint32_t idx_sh[64], sid_sh[64], key_sh[64];
+// Every workgroup recomputes the routing of the <= 8 tokens from the logits (route_token),
+// the stable sort of the <= 64 assignments and the table of distinct experts — a few
+// microseconds of one wave's work that saves a dependent kernel boundary — and workgroup
+// (0, 0) publishes them.  Workgroup (x, g) then computes rows 4x.. of the gate/up GEMV of
+// the g-th distinct expert for every token routed to it (SwiGLU epilogue).
+template <int BITS, int MT, int NC, int PER>
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
+  __shared__ uint32_t idx_sh[64], key_sh[64], so_sh[64], sid_sh[64];
+  __shared__ uint16_t sc_sh[64];
+  __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
+  __shared__ int rows_sh[MT], orows_sh[MT];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int A = p.A;
+  const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
   for (int t = wave; t < p.T; t += 4) {
     uint32_t my_idx, my_score;
     route_token<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score);
     if (lane < p.k) {
-      p.idx[t * p.k + lane] = my_idx;
-      p.scores[t * p.k + lane] = (uint16_t)my_score;
       idx_sh[t * p.k + lane] = my_idx;
+      sc_sh[t * p.k + lane] = (uint16_t)my_score;
     }
   }
   __syncthreads();
-  const int A = p.A;
   if (wave == 0) {
-    // stable sort of <= 64 assignments by (expert, slot): rank = number of smaller keys
+    // stable sort by (expert, slot): rank = number of smaller keys
     const uint32_t key = lane < A ? (idx_sh[lane] << 6) | (uint32_t)lane : 0xffffffffu;
     key_sh[lane] = key;
     __builtin_amdgcn_wave_barrier();
@@ -302,179 +310,191 @@ __global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
 #pragma unroll
     for (int b2 = 0; b2 < 64; ++b2) rank += key_sh[b2] < key;
     if (lane < A) {
-      p.sorted_order[rank] = (uint32_t)lane;
-      p.inverse_order[lane] = rank;
-      p.sorted_ids[rank] = key >> 6;
+      so_sh[rank] = (uint32_t)lane;
       sid_sh[rank] = key >> 6;
     }
-  }
-  __syncthreads();
-  if (wave == 0) {
-    // distinct experts in ascending order: group g = (expert, first sorted row, count)
+    __builtin_amdgcn_wave_barrier();
+    // distinct experts in ascending order: (expert, first sorted row, count)
     const uint32_t sid = lane < A ? sid_sh[lane] : 0xffffffffu;
     const bool start = lane < A && (lane == 0 || sid != sid_sh[lane - 1]);
     const uint64_t mask = __ballot(start);
+    const int gi = __popcll(mask & ((1ull << lane) - 1ull));
+    const uint64_t above = lane == 63 ? 0ull : (mask >> (lane + 1));
+    const int next = above ? lane + 1 + __ffsll((long long)above) - 1 : A;
     if (start) {
-      const int g = __popcll(mask & ((1ull << lane) - 1ull));
-      const uint64_t above = lane == 63 ? 0ull : (mask >> (lane + 1));
-      const int next = above ? lane + 1 + __ffsll((long long)above) - 1 : A;
-      p.g_expert[g] = sid;
-      p.g_start[g] = (uint32_t)lane;
-      p.g_count[g] = (uint32_t)(next - lane);
+      g_expert_sh[gi] = sid;
+      g_start_sh[gi] = (uint32_t)lane;
+      g_count_sh[gi] = (uint32_t)(next - lane);
     }
-    if (lane == 0) *p.n_groups = (uint32_t)__popcll(mask);
+    if (lane == 0) ng_sh = (uint32_t)__popcll(mask);
+    if (publish) {
+      if (lane < A) {
+        p.idx[lane] = idx_sh[lane];
+        p.scores[lane] = sc_sh[lane];
+        p.sorted_order[rank] = (uint32_t)lane;
+        p.inverse_order[lane] = rank;
+        p.sorted_ids[rank] = key >> 6;
+      }
+      if (start) {
+        p.g_expert[gi] = sid;
+        p.g_start[gi] = (uint32_t)lane;
+        p.g_count[gi] = (uint32_t)(next - lane);
+      }
+      if (lane == 0) *p.n_groups = (uint32_t)__popcll(mask);
+    }
   }
-  // expert offsets [E+2] (E+1: trailing out-of-range bucket, empty here)
-  for (int e = threadIdx.x; e <= p.E + 1; e += 256) {
-    uint32_t c = 0;
+  __syncthreads();
+  if (publish) {
+    // expert offsets [E+2] (E+1: trailing out-of-range bucket, empty here)
+    for (int e = threadIdx.x; e <= p.E + 1; e += 256) {
+      uint32_t c = 0;
 #pragma unroll
-    for (int i = 0; i < 64; ++i) c += (i < A) & (sid_sh[i] < (uint32_t)e);
-    p.offsets[e] = e <= p.E ? c : (uint32_t)A;
+      for (int i = 0; i < 64; ++i) c += (i < A) & (sid_sh[i] < (uint32_t)e);
+      p.offsets[e] = e <= p.E ? c : (uint32_t)A;
+    }
   }
-}
-
-// ---------------------------------------------------------------- D3: routed gate/up
-
-template <int BITS, int MT, int NC>
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
-  __shared__ int rows_sh[MT], orows_sh[MT];
   const int g = blockIdx.y;
-  const int ng = (int)*p.n_groups;
-  if (g >= ng || g >= p.max_groups) return;
-  const uint32_t e = p.g_expert[g], start = p.g_start[g], m = p.g_count[g];
-  if (e >= (uint32_t)p.E || start + m > (uint32_t)p.A || m > (uint32_t)MT || m == 0) return;
+  if (g >= (int)ng_sh) return;
+  const uint32_t e = g_expert_sh[g], start = g_start_sh[g], m = g_count_sh[g];
+  if (m > (uint32_t)MT) return;  // a token selects an expert at most once: m <= T <= MT
   if (threadIdx.x < MT) {
     const uint32_t i = threadIdx.x < m ? threadIdx.x : m - 1;
-    const uint32_t tok = p.sorted_order[start + i] / (uint32_t)p.k;
-    rows_sh[threadIdx.x] = (int)(tok < (uint32_t)p.T ? tok : 0u);
+    rows_sh[threadIdx.x] = (int)(so_sh[start + i] / (uint32_t)p.k);
     orows_sh[threadIdx.x] = (int)(start + i);
   }
   __syncthreads();
-  const int wave = threadIdx.x >> 6;
   const int r0 = (blockIdx.x * 4 + wave) * kRowsPerWave;
   if (r0 >= p.I) return;
   const int nrows = min(kRowsPerWave, p.I - r0);
   const int64_t wo = (int64_t)e * p.gu_w_es + (int64_t)r0 * p.gu_w_rs;
   const int64_t so = (int64_t)e * p.gu_sb_es + (int64_t)r0 * p.gu_sb_rs;
-  rows_task<BITS, MT, kRowsPerWave, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
-                                   p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows,
-                                   p.H / 32, p.gu_group, p.x, p.H, rows_sh, (int)m,
-                                   p.act + r0, p.act_ld, orows_sh);
+  rows_task<BITS, MT, kRowsPerWave, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so,
+                                              p.up_w + wo, p.up_s + so, p.up_b + so, p.gu_w_rs,
+                                              p.gu_sb_rs, nrows, p.H / 32, p.gu_group, p.x, p.H,
+                                              rows_sh, (int)m, p.act + r0, p.act_ld, orows_sh);
 }
 
-// ---------------------------------------------------------------- D4: down (routed + shared)
+// ---------------------------------------------------------------- D3: down + combine
 
-// One wave per (group, HR output rows).  Quarter q of the wave (one DPP row of 16 lanes)
-// takes rows 4*it + q; its 16 lanes split the row's input chunks (lane l16 takes chunks
-// l16, l16+16, ...).  Branch-free like rows_task.
-template <int BITS, int MT, int NC, int HR>
+// One wave per (4 output rows, token).  Quarter q of the wave (one DPP row of 16 lanes)
+// takes row 4x + q; its 16 lanes split the row's input chunks (lane l16 takes chunks l16,
+// l16+16, ...).  The wave computes the down rows of all the token's k experts and of the
+// shared expert, so the weighted combine (slot order) and the shared expert's gated add
+// happen in registers.  Tokens that share an expert read its rows once each; at <= 8
+// tokens over hundreds of experts such sharing is rare.  Branch-free: slots past k reuse
+// slot k-1 and are masked out of the combine, a missing shared expert reuses slot 0.
+template <int BITS, int NC, bool SORTED>
 __global__ __launch_bounds__(64) void decode_down_kernel(const DecodeArgs p) {
-  constexpr int IT = HR / 4;
-  __shared__ uint16_t res[MT][HR];
+  constexpr int KM = kDecodeMaxK, P = KM + 1;
   const int lane = threadIdx.x, l16 = lane & 15, q = lane >> 4;
-  const int g = blockIdx.y;
-  const int ng = (int)*p.n_groups;
-  const bool shared = p.Is > 0 && g == ng;
-  if (g > ng || g > p.max_groups || (g == ng && !shared)) return;
-  int rows[MT], m, nchunks, group;
-  const uint32_t *w;
-  const uint16_t *sc, *bi;
-  int64_t w_rs, sb_rs;
-  if (shared) {
-    m = p.T;
+  const int t = blockIdx.y, h = blockIdx.x * 4 + q;
+  const bool has_shared = p.Is > 0;
+  const uint32_t *wrow[P];
+  const uint16_t *srow[P], *brow[P], *xrow[P];
+  int nch[P], grp[P];
+  uint32_t orow[P];
+  float sc[KM];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) rows[t] = p.A + (t < m ? t : m - 1);
-    w = p.sd_w;
-    sc = p.sd_s;
-    bi = p.sd_b;
-    w_rs = p.sd_w_rs;
-    sb_rs = p.sd_sb_rs;
-    nchunks = p.Is / 32;
-    group = p.sd_group;
-  } else {
-    const uint32_t e = p.g_expert[g], start = p.g_start[g];
-    m = (int)p.g_count[g];
-    if (e >= (uint32_t)p.E || start + (uint32_t)m > (uint32_t)p.A || m > MT || m <= 0) return;
-#pragma unroll
-    for (int t = 0; t < MT; ++t) rows[t] = (int)start + (t < m ? t : m - 1);
-    w = p.down_w + (int64_t)e * p.dn_w_es;
-    sc = p.down_s + (int64_t)e * p.dn_sb_es;
-    bi = p.down_b + (int64_t)e * p.dn_sb_es;
-    w_rs = p.dn_w_rs;
-    sb_rs = p.dn_sb_rs;
-    nchunks = p.I / 32;
-    group = p.dn_group;
+  for (int j = 0; j < KM; ++j) {
+    const int a = t * p.k + (j < p.k ? j : p.k - 1);
+    const uint32_t e = p.idx[a];
+    const uint32_t r = p.inverse_order[a];
+    sc[j] = bf2f(p.scores[a]);
+    orow[j] = r;
+    wrow[j] = p.down_w + (int64_t)e * p.dn_w_es + (int64_t)h * p.dn_w_rs;
+    srow[j] = p.down_s + (int64_t)e * p.dn_sb_es + (int64_t)h * p.dn_sb_rs;
+    brow[j] = p.down_b + (int64_t)e * p.dn_sb_es + (int64_t)h * p.dn_sb_rs;
+    xrow[j] = p.act + (int64_t)r * p.act_ld;
+    nch[j] = p.I / 32;
+    grp[j] = p.dn_group;
   }
-  const int h0 = blockIdx.x * HR;
-  float acc[IT][MT];
+  if (has_shared) {
+    orow[KM] = (uint32_t)(p.A + t);
+    wrow[KM] = p.sd_w + (int64_t)h * p.sd_w_rs;
+    srow[KM] = p.sd_s + (int64_t)h * p.sd_sb_rs;
+    brow[KM] = p.sd_b + (int64_t)h * p.sd_sb_rs;
+    xrow[KM] = p.act + (int64_t)(p.A + t) * p.act_ld;
+    nch[KM] = p.Is / 32;
+    grp[KM] = p.sd_group;
+  } else {
+    orow[KM] = orow[0];
+    wrow[KM] = wrow[0];
+    srow[KM] = srow[0];
+    brow[KM] = brow[0];
+    xrow[KM] = xrow[0];
+    nch[KM] = nch[0];
+    grp[KM] = grp[0];
+  }
+  float acc[P];
 #pragma unroll
-  for (int it = 0; it < IT; ++it)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[it][t] = 0.0f;
+  for (int j = 0; j < P; ++j) acc[j] = 0.0f;
 #pragma unroll
   for (int cc = 0; cc < NC; ++cc) {
     const int craw = l16 + 16 * cc;
-    const bool cv = craw < nchunks;
-    const int c = cv ? craw : 0;
-    WChunk wch[IT];
+    WChunk wch[P];
+    XChunk xch[P];
 #pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int h = h0 + 4 * it + q;
-      load_wchunk<BITS>(wch[it], w + (int64_t)h * w_rs, sc + (int64_t)h * sb_rs,
-                        bi + (int64_t)h * sb_rs, c, group);
+    for (int j = 0; j < P; ++j) {
+      const int c = craw < nch[j] ? craw : 0;
+      load_wchunk<BITS>(wch[j], wrow[j], srow[j], brow[j], c, grp[j]);
+      load_xchunk<BITS>(xch[j], xrow[j] + c * 32);
     }
-    XChunk xa[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) load_xchunk<BITS>(xa[t], p.act + (int64_t)rows[t] * p.act_ld + c * 32);
+    for (int j = 0; j < P; ++j) {
+      const float d = chunk_dot<BITS>(wch[j], xch[j]);
+      acc[j] += craw < nch[j] ? d : 0.0f;
+    }
+  }
+  float v[KM];
 #pragma unroll
-    for (int it = 0; it < IT; ++it)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const float d = chunk_dot<BITS>(wch[it], xa[t]);
-        acc[it][t] += cv ? d : 0.0f;
-      }
+  for (int j = 0; j < KM; ++j) v[j] = round_bf(row_sum(acc[j]));
+  const float shared_v = round_bf(row_sum(acc[KM]));
+  if (l16 != 0) return;
+  const uint32_t sparse = combine_element<SORTED, KM>(v, sc, p.k);
+  uint32_t out = sparse;
+  if (has_shared) {
+    const float gate = round_bf(det_sigmoid(bf2f(p.z[t])));
+    out = shared_gated_add(sparse, shared_v, gate);
+    p.down_out[(int64_t)orow[KM] * p.H + h] = (uint16_t)f2bf(shared_v);
   }
 #pragma unroll
-  for (int it = 0; it < IT; ++it)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const float v = row_sum(acc[it][t]);
-      if (l16 == 0) res[t][4 * it + q] = (uint16_t)f2bf(v);
-    }
-  __syncthreads();
-  if (lane < HR) {
-    const int h = h0 + lane;
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-      if (t < m) p.down_out[(int64_t)rows[t] * p.H + h] = res[t][lane];
-  }
+  for (int j = 0; j < KM; ++j)
+    if (j < p.k) p.down_out[(int64_t)orow[j] * p.H + h] = (uint16_t)f2bf(v[j]);
+  p.sparse[(int64_t)t * p.H + h] = (uint16_t)sparse;
+  p.y[(int64_t)t * p.H + h] = (uint16_t)out;
 }
 
-constexpr int down_rows(int mt) { return mt <= 2 ? 16 : 8; }
-
-template <int BITS, int MT, int NC>
-void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT, NC>), dim3((a.I + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave), a.max_groups),
+template <int BITS, int MT, int NC, int PER>
+void launch_gate_up_per(const DecodeArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT, NC, PER>),
+                     dim3((a.I + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave), a.max_groups),
                      dim3(256), 0, s, a);
 }
 
 template <int BITS, int MT, int NC>
+void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s) {
+  const int per = (a.E + 63) / 64;
+  if (per <= 1) launch_gate_up_per<BITS, MT, NC, 1>(a, s);
+  else if (per <= 2) launch_gate_up_per<BITS, MT, NC, 2>(a, s);
+  else if (per <= 4) launch_gate_up_per<BITS, MT, NC, 4>(a, s);
+  else if (per <= 8) launch_gate_up_per<BITS, MT, NC, 8>(a, s);
+  else launch_gate_up_per<BITS, MT, NC, 16>(a, s);
+}
+
+template <int BITS, int NC>
 void launch_down_nc(const DecodeArgs &a, hipStream_t s) {
-  constexpr int HR = down_rows(MT);
-  hipLaunchKernelGGL((decode_down_kernel<BITS, MT, NC, HR>),
-                     dim3(a.H / HR, a.max_groups + (a.Is > 0 ? 1 : 0)), dim3(64), 0, s, a);
+  const dim3 grid(a.H / 4, a.T);
+  // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
+  if (a.A >= 64)
+    hipLaunchKernelGGL((decode_down_kernel<BITS, NC, true>), grid, dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_down_kernel<BITS, NC, false>), grid, dim3(64), 0, s, a);
 }
 
 template <int BITS, int MT>
 void launch_gate_up_mt(const DecodeArgs &a, hipStream_t s) {
   if (a.H <= 2048) launch_gate_up_nc<BITS, MT, 1>(a, s);
   else launch_gate_up_nc<BITS, MT, 2>(a, s);
-}
-
-template <int BITS, int MT>
-void launch_down_mt(const DecodeArgs &a, hipStream_t s) {
-  if (std::max(a.I, a.Is) <= 512) launch_down_nc<BITS, MT, 1>(a, s);
-  else launch_down_nc<BITS, MT, 2>(a, s);
 }
 
 template <int BITS>
@@ -486,11 +506,9 @@ void launch_gate_up(const DecodeArgs &a, int mt, hipStream_t s) {
 }
 
 template <int BITS>
-void launch_down(const DecodeArgs &a, int mt, hipStream_t s) {
-  if (mt == 1) launch_down_mt<BITS, 1>(a, s);
-  else if (mt == 2) launch_down_mt<BITS, 2>(a, s);
-  else if (mt == 4) launch_down_mt<BITS, 4>(a, s);
-  else launch_down_mt<BITS, 8>(a, s);
+void launch_down(const DecodeArgs &a, hipStream_t s) {
+  if (std::max(a.I, a.Is) <= 512) launch_down_nc<BITS, 1>(a, s);
+  else launch_down_nc<BITS, 2>(a, s);
 }
 
 template <int MT, int NC>
@@ -504,24 +522,13 @@ void launch_router(const DecodeArgs &a, int blocks, hipStream_t s) {
   else launch_router_nc<MT, 2>(a, blocks, s);
 }
 
-void launch_route(const DecodeArgs &a, hipStream_t s) {
-  const int per = (a.E + 63) / 64;
-  if (per <= 1) hipLaunchKernelGGL(decode_route_kernel<1>, dim3(1), dim3(256), 0, s, a);
-  else if (per <= 2) hipLaunchKernelGGL(decode_route_kernel<2>, dim3(1), dim3(256), 0, s, a);
-  else if (per <= 4) hipLaunchKernelGGL(decode_route_kernel<4>, dim3(1), dim3(256), 0, s, a);
-  else if (per <= 8) hipLaunchKernelGGL(decode_route_kernel<8>, dim3(1), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(decode_route_kernel<16>, dim3(1), dim3(256), 0, s, a);
-}
-
 }  // namespace
 
 bool decode_supported(const DecodeArgs &a) {
-  const int mt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8;
   return a.T >= 1 && a.T <= 8 && a.A <= 64 && a.router_w != nullptr && a.H % 32 == 0 &&
-         a.H % down_rows(mt) == 0 && a.H <= 4096 && a.I % 32 == 0 && a.I <= 1024 &&
-         a.Is % 32 == 0 && a.Is <= 1024 && a.E <= 1024 && a.k <= 64 &&
-         (a.gu_bits == 4 || a.gu_bits == 8) && (a.dn_bits == 4 || a.dn_bits == 8) &&
-         a.gu_group >= 32 && a.dn_group >= 32 &&
+         a.H <= 4096 && a.I % 32 == 0 && a.I <= 1024 && a.Is % 32 == 0 && a.Is <= 1024 &&
+         a.E <= 1024 && a.k >= 1 && a.k <= kDecodeMaxK && (a.gu_bits == 4 || a.gu_bits == 8) &&
+         (a.dn_bits == 4 || a.dn_bits == 8) && a.gu_group >= 32 && a.dn_group >= 32 &&
          (a.Is == 0 || (a.sd_bits == a.dn_bits && (a.sg_bits == 4 || a.sg_bits == 8) &&
                         (a.sz_bits == 4 || a.sz_bits == 8) && a.sd_group >= 32 &&
                         a.sg_group >= 32 && a.sz_group >= 32));
@@ -533,7 +540,7 @@ hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *m
   auto mark = [&]() {
     if (marks) (void)hipEventRecord(marks[stage++], s);
   };
-  // D1: router rows (4 experts per block), shared gate/up (16 rows per block), output gate
+  // D1: router rows (4 experts per block), shared gate/up, output gate
   const int blocks = a.router_blocks + a.shared_pair_blocks + (a.sz_w ? 1 : 0);
   mark();
   if (mt == 1) launch_router<1>(a, blocks, s);
@@ -543,18 +550,16 @@ hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *m
   hipError_t e = hipGetLastError();
   mark();
   if (e != hipSuccess) return e;
-  launch_route(a, s);
-  e = hipGetLastError();
-  mark();  // sorting happens inside the route kernel: the sort stage is empty here
+  // routing and sorting run inside the gate/up kernel: their stages are empty here
   mark();
-  if (e != hipSuccess) return e;
+  mark();
   if (a.gu_bits == 8) launch_gate_up<8>(a, mt, s);
   else launch_gate_up<4>(a, mt, s);
   e = hipGetLastError();
   mark();
   if (e != hipSuccess) return e;
-  if (a.dn_bits == 8) launch_down<8>(a, mt, s);
-  else launch_down<4>(a, mt, s);
+  if (a.dn_bits == 8) launch_down<8>(a, s);
+  else launch_down<4>(a, s);
   e = hipGetLastError();
   mark();
   return e;

@@ -102,12 +102,15 @@ struct DecodeArgs {
   uint32_t *n_groups, *g_expert, *g_start, *g_count;
   uint16_t *act, *down_out, *z;
   int64_t act_ld;
+  uint16_t *sparse, *y;  // outputs: weighted sum of the routed experts, block output
   int router_blocks, shared_pair_blocks, max_groups;
 };
 
 bool decode_supported(const DecodeArgs &a);
 constexpr int kDecodeRowsPerWave = 1;  // must match kRowsPerWave in decode.hip
-// launches the four decode kernels; marks (nullable) receives 6 stage boundaries
+constexpr int kDecodeMaxK = 8;         // experts per token the decode combine unrolls
+// launches the three decode kernels, combine included; marks (nullable) receives 6 stage
+// boundaries (router | route | sort | gate_up | down), the route and sort stages empty
 hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *marks);
 
 }  // namespace astro

@@ -235,6 +235,19 @@ def _check_block(ops, orc, L, x, what):
     assert np.array_equal(tr["sorted_order"], so) and np.array_equal(tr["inverse_order"], inv)
     assert np.array_equal(tr["sorted_ids"], sid) and np.array_equal(tr["expert_offsets"], off)
     assert tr["sorted_path"] == (A >= 64) == ref["used_sorted_path"]
+    # the combine is deterministic: bit-exact against the oracle's combine of the device's
+    # own expert outputs, scores and shared expert
+    eo = tr["expert_out_sorted"]
+    if tr["sorted_path"]:
+        sparse_ref = orc.sorted_weighted_sum(eo, tr["inverse_order"], tr["scores"])
+    else:
+        sparse_ref = orc.unsorted_weighted_sum(eo[tr["inverse_order"]].reshape(T, L.top_k, -1), tr["scores"])
+    assert np.array_equal(tr["sparse"], sparse_ref), what + " sparse combine"
+    if L.shared_intermediate:
+        assert np.array_equal(y, orc.combine_shared(sparse_ref, tr["shared_out"], tr["shared_gate_logits"])), \
+            what + " shared combine"
+    else:
+        assert np.array_equal(y, sparse_ref), what + " combine"
     # intermediates and output
     act = tr["activated_sorted"][inv]  # back to assignment order
     stats = {"act": assert_bf16_close(act, ref["activated"], what + " activated")}
