@@ -20,10 +20,9 @@ __device__ __forceinline__ float bf_hi(uint32_t pair) { return __uint_as_float(p
 
 // IEEE round-to-nearest-even fp32 -> bf16 on the bit pattern (NaN stays quiet NaN).
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : rounded;
 }
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
@@ -33,14 +32,13 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
 // exp(x): Cody-Waite reduction x = n ln2 + r (|r| <= ln2/2), degree-7 Taylor polynomial
 // with explicit fma, exact power-of-two scale; e^x below e^-80 is 0 so no subnormal is
 // produced.  Only IEEE mul/fma/rint are used, so the host restatement of the same
-// steps returns identical bits.
+// steps returns identical bits.  Branch-free: the argument is clamped to [-81, 89] for the
+// arithmetic and the special cases (NaN, overflow, underflow) are selected at the end.
 __device__ __forceinline__ float det_expf(float x) {
 #pragma clang fp contract(off)
-  if (x != x) return x;
-  if (x > 88.72283172607421875f) return __builtin_inff();
-  if (x < -80.0f) return 0.0f;
-  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
-  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -81.0f), 89.0f);
+  const float n = __builtin_rintf(xc * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, xc);
   r = __builtin_fmaf(-n, 1.42860676533018704e-6f, r);
   float p = (float)(1.0 / 5040.0);
   p = __builtin_fmaf(p, r, (float)(1.0 / 720.0));
@@ -51,11 +49,13 @@ __device__ __forceinline__ float det_expf(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
   int ni = (int)n;
-  if (ni > 127) {
-    p = p * 2.0f;
-    ni -= 1;
-  }
-  return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+  const bool big = ni > 127;  // 2^128 is not a float: scale by 2 * 2^127
+  p = big ? p * 2.0f : p;
+  ni = big ? ni - 1 : ni;
+  float res = p * __uint_as_float((uint32_t)(ni + 127) << 23);
+  res = x > 88.72283172607421875f ? __builtin_inff() : res;
+  res = x < -80.0f ? 0.0f : res;
+  return x != x ? x : res;
 }
 
 __device__ __forceinline__ float det_sigmoid(float v) {
@@ -161,6 +161,29 @@ __device__ __forceinline__ float wave_sum_fast(float v) {
   const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
   const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
   return (r0 + r1) + (r2 + r3);
+}
+
+// Maximum over the wave of unsigned keys with DPP only (quad permutes, row rotations, then
+// row_bcast:15 / row_bcast:31 fold the rows into lane 63) and one readlane: a single
+// vector-to-scalar transfer.  Uniform result.
+__device__ __forceinline__ uint32_t wave_max_u32_bcast(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, false));   // lane ^ 1
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, false));   // lane ^ 2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false));  // row_ror:4
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false));  // row_ror:8
+  // rows 1 and 3 take lane 15 / 47 of the row below; rows 2 and 3 then take lane 31
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xa, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xc, 0xf, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ float wave_max_bcast(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xa, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xc, 0xf, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Maximum over the wave of unsigned keys; uniform result.

@@ -1,12 +1,13 @@
 // Decode path of the block (T <= 8 tokens, T*k <= 64 assignments): wavefront GEMVs
 // instead of MFMA tiles, three kernels per layer:
-//   D1  router GEMV (one wave per expert row) + the shared expert's gate/up + SwiGLU and
-//       its output gate — all the work that does not depend on routing;
-//   D2  routing (softmax/top-k, the sort of the assignments, the distinct-expert table),
-//       recomputed by every workgroup, then the routed gate/up GEMV + SwiGLU: one wave
-//       per (gate row, up row) pair of one selected expert, every token routed to it;
+//   D1  router GEMV (one wave per expert row);
+//   D2  the shared expert's gate/up + SwiGLU and its output gate (no routing needed), and
+//       routing (softmax/top-k, the sort of the assignments, the distinct-expert table),
+//       recomputed by every routed workgroup, then the routed gate/up GEMV + SwiGLU: one
+//       wave per (gate row, up row) pair of one selected expert, every token routed to it;
 //   D3  per token: down GEMV rows of its k experts and of the shared expert (16 lanes per
-//       row), then the weighted combine and the shared expert's gated add in registers.
+//       row, the participants spread over 4 waves), then the weighted combine and the
+//       shared expert's gated add.
 // Affine rows are read once per distinct expert with 16 B per lane loads.  4-bit codes are
 // turned into bf16 pairs (128 + q) with one and/or per pair and multiplied by
 // v_dot2_f32_bf16; the per-group affine terms are applied per 32-input chunk:
@@ -47,17 +48,25 @@ struct XChunk {
   float sum;
 };
 
-template <int BITS>
-__device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *src) {
-  uint32_t r[16];
+struct XRaw {
+  u32x4 v[4];
+};
+
+__device__ __forceinline__ void load_xraw(XRaw &xr, const uint16_t *src) {
   const u32x4 *q = (const u32x4 *)src;
 #pragma unroll
+  for (int i = 0; i < 4; ++i) xr.v[i] = q[i];
+}
+
+template <int BITS>
+__device__ __forceinline__ void convert_xchunk(XChunk &xc, const XRaw &xr) {
+  uint32_t r[16];
+#pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const u32x4 v = q[i];
-    r[4 * i] = v[0];
-    r[4 * i + 1] = v[1];
-    r[4 * i + 2] = v[2];
-    r[4 * i + 3] = v[3];
+    r[4 * i] = xr.v[i][0];
+    r[4 * i + 1] = xr.v[i][1];
+    r[4 * i + 2] = xr.v[i][2];
+    r[4 * i + 3] = xr.v[i][3];
   }
   float s = 0.0f;
 #pragma unroll
@@ -76,6 +85,13 @@ __device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *src) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) xc.p[j] = r[j];
   }
+}
+
+template <int BITS>
+__device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *src) {
+  XRaw xr;
+  load_xraw(xr, src);
+  convert_xchunk<BITS>(xc, xr);
 }
 
 // codes of one 32-input chunk of one weight row: 4 words (4-bit) or 8 words (8-bit)
@@ -187,114 +203,121 @@ __device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs
   }
 }
 
-// ---------------------------------------------------------------- D1: router + shared
+// ---------------------------------------------------------------- D1: router
 
+// Router GEMV: one wave per expert row (bf16 weights), every token.
 template <int MT, int NC>
-__global__ __launch_bounds__(256) void decode_router_shared_kernel(const DecodeArgs p) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __shared__ int rows_sh[MT], orows_sh[MT];
-  if (threadIdx.x < MT) {
-    const int t = threadIdx.x < p.T ? threadIdx.x : p.T - 1;
-    rows_sh[threadIdx.x] = t;
-    orows_sh[threadIdx.x] = p.A + t;
-  }
-  __syncthreads();
-  const int b = blockIdx.x;
+__global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) {
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + wave;
+  if (e >= p.E) return;
   const int nchunks = p.H / 32;
-  if (b < p.router_blocks) {
-    const int e = b * 4 + wave;
-    if (e >= p.E) return;
-    const uint16_t *w = p.router_w + (int64_t)e * p.H;
-    float acc[MT];
+  const uint16_t *w = p.router_w + (int64_t)e * p.H;
+  float acc[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+  for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
-      const int craw = lane + 64 * cc;
-      const bool cv = craw < nchunks;
-      const int c = cv ? craw : 0;
-      const u32x4 *wp = (const u32x4 *)(w + c * 32);
-      u32x4 wv[4], xv[MT][4];
+  for (int cc = 0; cc < NC; ++cc) {
+    const int craw = lane + 64 * cc;
+    const bool cv = craw < nchunks;
+    const int c = cv ? craw : 0;
+    const u32x4 *wp = (const u32x4 *)(w + c * 32);
+    u32x4 wv[4], xv[MT][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wv[i] = wp[i];
+    for (int i = 0; i < 4; ++i) wv[i] = wp[i];
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const u32x4 *xp = (const u32x4 *)(p.x + (int64_t)rows_sh[t] * p.H + c * 32);
+    for (int t = 0; t < MT; ++t) {
+      const int tr = t < p.T ? t : p.T - 1;
+      const u32x4 *xp = (const u32x4 *)(p.x + (int64_t)tr * p.H + c * 32);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xv[t][i] = xp[i];
-      }
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        float a = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) a = dot2(wv[i][j], xv[t][i][j], a);
-        acc[t] += cv ? a : 0.0f;
-      }
+      for (int i = 0; i < 4; ++i) xv[t][i] = xp[i];
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const float v = wave_sum_fast(acc[t]);
-      if (lane == 0 && t < p.T) {
-        uint32_t o = f2bf(v);
-        if (p.router_bias) o = f2bf(bf2f(o) + bf2f(p.router_bias[e]));
-        p.logits[(int64_t)t * p.E + e] = (uint16_t)o;
-      }
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a = dot2(wv[i][j], xv[t][i][j], a);
+      acc[t] += cv ? a : 0.0f;
     }
-    return;
   }
-  const int sb = b - p.router_blocks;
-  if (sb < p.shared_pair_blocks) {
-    // shared expert gate/up + SwiGLU
-    const int r0 = (sb * 4 + wave) * kRowsPerWave;
-    if (r0 >= p.Is) return;
-    const int nrows = min(kRowsPerWave, p.Is - r0);
-    if (p.sg_bits == 4)
-      rows_task<4, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
-                                               p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
-                                               p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
-                                               p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
-                                               p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
-                                               orows_sh);
-    else
-      rows_task<8, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
-                                               p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
-                                               p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
-                                               p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
-                                               p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
-                                               orows_sh);
-    return;
+  const float bias = p.router_bias ? bf2f(p.router_bias[e]) : 0.0f;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const float v = wave_sum_fast(acc[t]);
+    if (lane == 0 && t < p.T) {
+      uint32_t o = f2bf(v);
+      if (p.router_bias) o = f2bf(bf2f(o) + bias);
+      p.logits[(int64_t)t * p.E + e] = (uint16_t)o;
+    }
   }
-  // the shared expert's output gate (one row) -> z[t]
-  if (wave != 0 || !p.sz_w) return;
-  if (p.sz_bits == 4)
-    rows_task<4, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
-                                   nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
-  else
-    rows_task<8, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
-                                   nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
 }
 
-// ---------------------------------------------------------------- D2: route + routed gate/up
+// ---------------------------------------------------------------- D2: route + gate/up
 
-// Every workgroup recomputes the routing of the <= 8 tokens from the logits (route_token),
-// the stable sort of the <= 64 assignments and the table of distinct experts — a few
-// microseconds of one wave's work that saves a dependent kernel boundary — and workgroup
-// (0, 0) publishes them.  Workgroup (x, g) then computes rows 4x.. of the gate/up GEMV of
-// the g-th distinct expert for every token routed to it (SwiGLU epilogue).
+// Workgroups (x, 0): the shared expert, which needs no routing — x < shared_pair_blocks
+// computes 4 (gate row, up row) pairs with the SwiGLU epilogue, x == shared_pair_blocks
+// the output gate z.  Workgroups (x, g + 1): every one recomputes the routing of the <= 8
+// tokens from the logits (route_token), the stable sort of the <= 64 assignments and the
+// table of distinct experts — a few microseconds of one wave's work that saves a dependent
+// kernel boundary — and workgroup (0, 1) publishes them; then it computes rows 4x.. of the
+// gate/up GEMV of the g-th distinct expert for every token routed to it (SwiGLU epilogue).
 template <int BITS, int MT, int NC, int PER>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
-  __shared__ uint32_t idx_sh[64], key_sh[64], so_sh[64], sid_sh[64];
+  constexpr int KM = kDecodeMaxK, AMAX = MT * KM;
+  __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
+  __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
+  __shared__ __attribute__((aligned(16))) uint32_t route_sh[4][KM];
   __shared__ uint16_t sc_sh[64];
   __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
   __shared__ int rows_sh[MT], orows_sh[MT];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+  const int nchunks = p.H / 32;
+  if (blockIdx.y == 0) {
+    if (threadIdx.x < MT) {
+      const int t = threadIdx.x < p.T ? threadIdx.x : p.T - 1;
+      rows_sh[threadIdx.x] = t;
+      orows_sh[threadIdx.x] = p.A + t;
+    }
+    __syncthreads();
+    const int sb = blockIdx.x;
+    if (sb < p.shared_pair_blocks) {
+      const int r0 = (sb * 4 + wave) * kRowsPerWave;
+      if (r0 >= p.Is) return;
+      const int nrows = min(kRowsPerWave, p.Is - r0);
+      if (p.sg_bits == 4)
+        rows_task<4, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
+                                                 p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
+                                                 p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
+                                                 p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
+                                                 p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
+                                                 orows_sh);
+      else
+        rows_task<8, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
+                                                 p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
+                                                 p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
+                                                 p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
+                                                 p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
+                                                 orows_sh);
+      return;
+    }
+    if (sb != p.shared_pair_blocks || wave != 0 || !p.sz_w) return;
+    if (p.sz_bits == 4)
+      rows_task<4, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
+                                     nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
+    else
+      rows_task<8, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
+                                     nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
+    return;
+  }
+  if ((int)blockIdx.x * 4 * kRowsPerWave >= p.I) return;
   const int A = p.A;
-  const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
+  const bool publish = blockIdx.x == 0 && blockIdx.y == 1;
   for (int t = wave; t < p.T; t += 4) {
     uint32_t my_idx, my_score;
-    route_token<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, my_idx, my_score);
+    route_token<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, route_sh[wave],
+                         my_idx, my_score);
     if (lane < p.k) {
       idx_sh[t * p.k + lane] = my_idx;
       sc_sh[t * p.k + lane] = (uint16_t)my_score;
@@ -306,9 +329,14 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
     const uint32_t key = lane < A ? (idx_sh[lane] << 6) | (uint32_t)lane : 0xffffffffu;
     key_sh[lane] = key;
     __builtin_amdgcn_wave_barrier();
+    // the AMAX >= A keys in broadcast reads, issued before any comparison
+    u32x4 kv[AMAX / 4];
+#pragma unroll
+    for (int b2 = 0; b2 < AMAX / 4; ++b2) kv[b2] = ((const u32x4 *)key_sh)[b2];
     uint32_t rank = 0;
 #pragma unroll
-    for (int b2 = 0; b2 < 64; ++b2) rank += key_sh[b2] < key;
+    for (int b2 = 0; b2 < AMAX / 4; ++b2)
+      rank += (kv[b2][0] < key) + (kv[b2][1] < key) + (kv[b2][2] < key) + (kv[b2][3] < key);
     if (lane < A) {
       so_sh[rank] = (uint32_t)lane;
       sid_sh[rank] = key >> 6;
@@ -349,11 +377,11 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
     for (int e = threadIdx.x; e <= p.E + 1; e += 256) {
       uint32_t c = 0;
 #pragma unroll
-      for (int i = 0; i < 64; ++i) c += (i < A) & (sid_sh[i] < (uint32_t)e);
+      for (int i = 0; i < AMAX; ++i) c += (i < A) & (sid_sh[i] < (uint32_t)e);
       p.offsets[e] = e <= p.E ? c : (uint32_t)A;
     }
   }
-  const int g = blockIdx.y;
+  const int g = blockIdx.y - 1;
   if (g >= (int)ng_sh) return;
   const uint32_t e = g_expert_sh[g], start = g_start_sh[g], m = g_count_sh[g];
   if (m > (uint32_t)MT) return;  // a token selects an expert at most once: m <= T <= MT
@@ -370,105 +398,126 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
   const int64_t so = (int64_t)e * p.gu_sb_es + (int64_t)r0 * p.gu_sb_rs;
   rows_task<BITS, MT, kRowsPerWave, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so,
                                               p.up_w + wo, p.up_s + so, p.up_b + so, p.gu_w_rs,
-                                              p.gu_sb_rs, nrows, p.H / 32, p.gu_group, p.x, p.H,
+                                              p.gu_sb_rs, nrows, nchunks, p.gu_group, p.x, p.H,
                                               rows_sh, (int)m, p.act + r0, p.act_ld, orows_sh);
 }
 
 // ---------------------------------------------------------------- D3: down + combine
 
-// One wave per (4 output rows, token).  Quarter q of the wave (one DPP row of 16 lanes)
-// takes row 4x + q; its 16 lanes split the row's input chunks (lane l16 takes chunks l16,
-// l16+16, ...).  The wave computes the down rows of all the token's k experts and of the
-// shared expert, so the weighted combine (slot order) and the shared expert's gated add
-// happen in registers.  Tokens that share an expert read its rows once each; at <= 8
-// tokens over hundreds of experts such sharing is rare.  Branch-free: slots past k reuse
-// slot k-1 and are masked out of the combine, a missing shared expert reuses slot 0.
+// One workgroup of 4 waves per (4 output rows, token).  The token's k experts and the
+// shared expert are P = kDecodeMaxK + 1 participant rows per output row; wave w computes
+// participants w, w+4, w+8.  Quarter q of a wave (one DPP row of 16 lanes) takes output
+// row 4x + q and its 16 lanes split the input chunks (lane l16 takes chunks l16, l16+16,
+// ...).  The rounded participant values meet in LDS, where wave 0 forms the weighted
+// combine (slot order) and the shared expert's gated add.  Branch-free: participants past
+// k, or a missing shared expert, reuse slot 0's rows and are masked out.
 template <int BITS, int NC, bool SORTED>
-__global__ __launch_bounds__(64) void decode_down_kernel(const DecodeArgs p) {
-  constexpr int KM = kDecodeMaxK, P = KM + 1;
-  const int lane = threadIdx.x, l16 = lane & 15, q = lane >> 4;
+__global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
+  constexpr int KM = kDecodeMaxK, P = KM + 1, PW = (P + 3) / 4;
+  __shared__ float vals[4][4 * PW];
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
   const int t = blockIdx.y, h = blockIdx.x * 4 + q;
   const bool has_shared = p.Is > 0;
-  const uint32_t *wrow[P];
-  const uint16_t *srow[P], *brow[P], *xrow[P];
-  int nch[P], grp[P];
-  uint32_t orow[P];
+  // loads the combine needs, issued first (a missing shared expert reads a score instead)
+  const uint16_t zbits = has_shared ? p.z[t] : p.scores[0];
   float sc[KM];
 #pragma unroll
-  for (int j = 0; j < KM; ++j) {
-    const int a = t * p.k + (j < p.k ? j : p.k - 1);
-    const uint32_t e = p.idx[a];
-    const uint32_t r = p.inverse_order[a];
-    sc[j] = bf2f(p.scores[a]);
-    orow[j] = r;
-    wrow[j] = p.down_w + (int64_t)e * p.dn_w_es + (int64_t)h * p.dn_w_rs;
-    srow[j] = p.down_s + (int64_t)e * p.dn_sb_es + (int64_t)h * p.dn_sb_rs;
-    brow[j] = p.down_b + (int64_t)e * p.dn_sb_es + (int64_t)h * p.dn_sb_rs;
-    xrow[j] = p.act + (int64_t)r * p.act_ld;
-    nch[j] = p.I / 32;
-    grp[j] = p.dn_group;
-  }
-  if (has_shared) {
-    orow[KM] = (uint32_t)(p.A + t);
-    wrow[KM] = p.sd_w + (int64_t)h * p.sd_w_rs;
-    srow[KM] = p.sd_s + (int64_t)h * p.sd_sb_rs;
-    brow[KM] = p.sd_b + (int64_t)h * p.sd_sb_rs;
-    xrow[KM] = p.act + (int64_t)(p.A + t) * p.act_ld;
-    nch[KM] = p.Is / 32;
-    grp[KM] = p.sd_group;
-  } else {
-    orow[KM] = orow[0];
-    wrow[KM] = wrow[0];
-    srow[KM] = srow[0];
-    brow[KM] = brow[0];
-    xrow[KM] = xrow[0];
-    nch[KM] = nch[0];
-    grp[KM] = grp[0];
-  }
-  float acc[P];
+  for (int j = 0; j < KM; ++j) sc[j] = bf2f(p.scores[t * p.k + (j < p.k ? j : p.k - 1)]);
+
+  // participant rows, selected without branches
+  const uint32_t *sd_w = has_shared ? p.sd_w : p.down_w;
+  const uint16_t *sd_s = has_shared ? p.sd_s : p.down_s;
+  const uint16_t *sd_b = has_shared ? p.sd_b : p.down_b;
+  const int64_t sd_w_rs = has_shared ? p.sd_w_rs : p.dn_w_rs;
+  const int64_t sd_sb_rs = has_shared ? p.sd_sb_rs : p.dn_sb_rs;
+  const int sd_nch = has_shared ? p.Is / 32 : p.I / 32;
+  const int sd_group = has_shared ? p.sd_group : p.dn_group;
+  uint32_t e[PW], r[PW];
 #pragma unroll
-  for (int j = 0; j < P; ++j) acc[j] = 0.0f;
+  for (int i = 0; i < PW; ++i) {
+    const int j = wave + 4 * i;
+    const int a = t * p.k + (j < p.k ? j : 0);
+    e[i] = p.idx[a];
+    r[i] = p.inverse_order[a];
+  }
+  const uint32_t *wrow[PW];
+  const uint16_t *srow[PW], *brow[PW];
+  const uint16_t *xrow[PW];
+  int nch[PW], grp[PW];
+  uint32_t orow[PW];
+  bool live[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int j = wave + 4 * i;
+    const bool shared = j == KM && has_shared;
+    live[i] = (j < KM && j < p.k) || shared;
+    orow[i] = shared ? (uint32_t)(p.A + t) : r[i];
+    const uint32_t *wb = shared ? sd_w : p.down_w + (int64_t)e[i] * p.dn_w_es;
+    const uint16_t *sb = shared ? sd_s : p.down_s + (int64_t)e[i] * p.dn_sb_es;
+    const uint16_t *bb = shared ? sd_b : p.down_b + (int64_t)e[i] * p.dn_sb_es;
+    const int64_t wrs = shared ? sd_w_rs : p.dn_w_rs;
+    const int64_t sbrs = shared ? sd_sb_rs : p.dn_sb_rs;
+    wrow[i] = wb + (int64_t)h * wrs;
+    srow[i] = sb + (int64_t)h * sbrs;
+    brow[i] = bb + (int64_t)h * sbrs;
+    xrow[i] = p.act + (int64_t)orow[i] * p.act_ld;
+    nch[i] = shared ? sd_nch : p.I / 32;
+    grp[i] = shared ? sd_group : p.dn_group;
+  }
+  float acc[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) acc[i] = 0.0f;
 #pragma unroll
   for (int cc = 0; cc < NC; ++cc) {
     const int craw = l16 + 16 * cc;
-    WChunk wch[P];
-    XChunk xch[P];
+    // every load of the chunk step first, then the arithmetic
+    WChunk wch[PW];
+    XRaw xr[PW];
 #pragma unroll
-    for (int j = 0; j < P; ++j) {
-      const int c = craw < nch[j] ? craw : 0;
-      load_wchunk<BITS>(wch[j], wrow[j], srow[j], brow[j], c, grp[j]);
-      load_xchunk<BITS>(xch[j], xrow[j] + c * 32);
+    for (int i = 0; i < PW; ++i) {
+      const int c = craw < nch[i] ? craw : 0;
+      load_wchunk<BITS>(wch[i], wrow[i], srow[i], brow[i], c, grp[i]);
+      load_xraw(xr[i], xrow[i] + c * 32);
     }
+    // keep the scheduler from interleaving the first participant's arithmetic (and its
+    // waits) with the later participants' loads
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < P; ++j) {
-      const float d = chunk_dot<BITS>(wch[j], xch[j]);
-      acc[j] += craw < nch[j] ? d : 0.0f;
+    for (int i = 0; i < PW; ++i) {
+      XChunk xc;
+      convert_xchunk<BITS>(xc, xr[i]);
+      const float d = chunk_dot<BITS>(wch[i], xc);
+      acc[i] += craw < nch[i] ? d : 0.0f;
     }
   }
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const float v = round_bf(row_sum(acc[i]));
+    if (l16 == 0) {
+      vals[q][wave + 4 * i] = v;
+      if (live[i]) p.down_out[(int64_t)orow[i] * p.H + h] = (uint16_t)f2bf(v);
+    }
+  }
+  __syncthreads();
+  if (wave != 0 || l16 != 0) return;
   float v[KM];
 #pragma unroll
-  for (int j = 0; j < KM; ++j) v[j] = round_bf(row_sum(acc[j]));
-  const float shared_v = round_bf(row_sum(acc[KM]));
-  if (l16 != 0) return;
+  for (int j = 0; j < KM; ++j) v[j] = vals[q][j];
   const uint32_t sparse = combine_element<SORTED, KM>(v, sc, p.k);
   uint32_t out = sparse;
-  if (has_shared) {
-    const float gate = round_bf(det_sigmoid(bf2f(p.z[t])));
-    out = shared_gated_add(sparse, shared_v, gate);
-    p.down_out[(int64_t)orow[KM] * p.H + h] = (uint16_t)f2bf(shared_v);
-  }
-#pragma unroll
-  for (int j = 0; j < KM; ++j)
-    if (j < p.k) p.down_out[(int64_t)orow[j] * p.H + h] = (uint16_t)f2bf(v[j]);
+  if (has_shared) out = shared_gated_add(sparse, vals[q][KM], round_bf(det_sigmoid(bf2f(zbits))));
   p.sparse[(int64_t)t * p.H + h] = (uint16_t)sparse;
   p.y[(int64_t)t * p.H + h] = (uint16_t)out;
 }
 
 template <int BITS, int MT, int NC, int PER>
 void launch_gate_up_per(const DecodeArgs &a, hipStream_t s) {
+  // x: routed row blocks, or the shared expert's pair blocks and its output-gate block
+  const int routed_x = (a.I + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave);
+  const int shared_x = a.Is > 0 ? a.shared_pair_blocks + 1 : 0;
   hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT, NC, PER>),
-                     dim3((a.I + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave), a.max_groups),
-                     dim3(256), 0, s, a);
+                     dim3(std::max(routed_x, shared_x), a.max_groups + 1), dim3(256), 0, s, a);
 }
 
 template <int BITS, int MT, int NC>
@@ -486,9 +535,9 @@ void launch_down_nc(const DecodeArgs &a, hipStream_t s) {
   const dim3 grid(a.H / 4, a.T);
   // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
   if (a.A >= 64)
-    hipLaunchKernelGGL((decode_down_kernel<BITS, NC, true>), grid, dim3(64), 0, s, a);
+    hipLaunchKernelGGL((decode_down_kernel<BITS, NC, true>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((decode_down_kernel<BITS, NC, false>), grid, dim3(64), 0, s, a);
+    hipLaunchKernelGGL((decode_down_kernel<BITS, NC, false>), grid, dim3(256), 0, s, a);
 }
 
 template <int BITS, int MT>
@@ -513,7 +562,7 @@ void launch_down(const DecodeArgs &a, hipStream_t s) {
 
 template <int MT, int NC>
 void launch_router_nc(const DecodeArgs &a, int blocks, hipStream_t s) {
-  hipLaunchKernelGGL((decode_router_shared_kernel<MT, NC>), dim3(blocks), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((decode_router_kernel<MT, NC>), dim3(blocks), dim3(256), 0, s, a);
 }
 
 template <int MT>
@@ -540,8 +589,8 @@ hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *m
   auto mark = [&]() {
     if (marks) (void)hipEventRecord(marks[stage++], s);
   };
-  // D1: router rows (4 experts per block), shared gate/up, output gate
-  const int blocks = a.router_blocks + a.shared_pair_blocks + (a.sz_w ? 1 : 0);
+  // D1: router rows (4 experts per block)
+  const int blocks = a.router_blocks;
   mark();
   if (mt == 1) launch_router<1>(a, blocks, s);
   else if (mt == 2) launch_router<2>(a, blocks, s);

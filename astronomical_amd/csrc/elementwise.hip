@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void qgemv_rows_kernel(
     const uint16_t *__restrict__ sc, const uint16_t *__restrict__ bi, int N, int group,
     uint16_t *__restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int item = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (item >= T * N) return;
   const int t = item / N, n = item % N;
   const int wpr = K * BITS / 32;          // words per row

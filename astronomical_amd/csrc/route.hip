@@ -9,16 +9,17 @@ namespace astro {
 namespace {
 
 // One wave per token (route_token in route_dev.h).
-template <int PER>
+template <int PER, int KMAX>
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restrict__ logits,
                                                          int T, int E, int k, int normalize,
                                                          uint32_t *__restrict__ idx,
                                                          uint16_t *__restrict__ scores) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) uint32_t sh[4][KMAX];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
   uint32_t my_idx, my_score;
-  route_token<PER>(logits + (int64_t)t * E, E, k, normalize, my_idx, my_score);
+  route_token<PER, KMAX>(logits + (int64_t)t * E, E, k, normalize, sh[wave], my_idx, my_score);
   if (lane < k) {
     idx[(int64_t)t * k + lane] = my_idx;
     scores[(int64_t)t * k + lane] = (uint16_t)my_score;
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(kScatterThreads) void sort_scatter_kernel(
     for (int j = 0; j < 16; ++j) mine += (base + j < a1) && bucket_of(v[j]) == bucket;
   }
   // block exclusive scan of `mine`
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   uint32_t incl = mine;
   for (int off = 1; off < 64; off <<= 1) {
     const uint32_t o = (uint32_t)__shfl_up((int)incl, off, kWave);
@@ -124,21 +125,30 @@ __global__ __launch_bounds__(kScatterThreads) void sort_scatter_kernel(
 
 }  // namespace
 
-hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
-                             uint32_t *idx, uint16_t *scores, hipStream_t s) {
-  if (T <= 0) return hipSuccess;
+template <int KMAX>
+void launch_route_k(const uint16_t *logits, int T, int E, int k, int normalize, uint32_t *idx,
+                    uint16_t *scores, hipStream_t s) {
   const dim3 grid((T + 3) / 4), block(256);
   const int per = (E + 63) / 64;
   if (per <= 1)
-    hipLaunchKernelGGL(route_topk_kernel<1>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<1, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
   else if (per <= 2)
-    hipLaunchKernelGGL(route_topk_kernel<2>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<2, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
   else if (per <= 4)
-    hipLaunchKernelGGL(route_topk_kernel<4>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<4, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
   else if (per <= 8)
-    hipLaunchKernelGGL(route_topk_kernel<8>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<8, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
   else
-    hipLaunchKernelGGL(route_topk_kernel<16>, grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<16, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+}
+
+hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
+                             uint32_t *idx, uint16_t *scores, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  // KMAX bounds the renormalisation's unrolled slice sum
+  if (k <= 8) launch_route_k<8>(logits, T, E, k, normalize, idx, scores, s);
+  else if (k <= 16) launch_route_k<16>(logits, T, E, k, normalize, idx, scores, s);
+  else launch_route_k<64>(logits, T, E, k, normalize, idx, scores, s);
   return hipGetLastError();
 }
 
