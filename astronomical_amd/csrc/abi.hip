@@ -284,18 +284,29 @@ hipError_t run_shared(const astro_moe_layer &L, const uint16_t *x, int T, uint16
                            z, s);
 }
 
-// The block's launch sequence.  `marks` (nullable) receives ASTRO_MOE_STAGES + 1 event
-// records at the stage boundaries: router, route, sort, gate/up, down, shared, combine.
+// Per-stage device times for the attributed entry point: a start and a stop event per
+// stage (router, route, sort, gate/up, down, shared, combine).  Kernels that make up a
+// stage on their own are launched with the events attached to the kernel itself
+// (hipExtLaunchKernelGGL), other stages are bracketed by event records; stages with no
+// work of their own (routing inside the decode gate/up kernel, for one) stay unused.
+struct StageClock {
+  hipEvent_t *ev;  // 2 * ASTRO_MOE_STAGES: start, stop
+  hipStream_t s;
+  bool used[ASTRO_MOE_STAGES];
+  void begin(int i) {
+    used[i] = true;
+    (void)hipEventRecord(ev[2 * i], s);
+  }
+  void end(int i) { (void)hipEventRecord(ev[2 * i + 1], s); }
+};
+
+// The block's launch sequence; clock (nullable) collects per-stage times.
 int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, uint16_t *y,
-              void *workspace, size_t workspace_bytes, void *stream, hipEvent_t *marks) {
+              void *workspace, size_t workspace_bytes, void *stream, StageClock *clock) {
   int rc = check_layer(kBlockOp, layer);
   if (rc) return rc;
   if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
-  if (tokens == 0) {
-    if (marks)
-      for (int i = 0; i <= ASTRO_MOE_STAGES; ++i) (void)hipEventRecord(marks[i], (hipStream_t)stream);
-    return ok();
-  }
+  if (tokens == 0) return ok();
   if (!x || !y) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "hidden states and output must be non-null");
   const astro_moe_layer &L = *layer;
   const Layout o = block_layout(L, tokens);
@@ -319,9 +330,11 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   uint16_t *eout = (uint16_t *)at(o.eout);
   uint16_t *sparse = (uint16_t *)at(o.sparse);
 
-  int stage = 0;
-  auto mark = [&]() {
-    if (marks) (void)hipEventRecord(marks[stage++], s);
+  auto begin = [&](int i) {
+    if (clock) clock->begin(i);
+  };
+  auto end = [&](int i) {
+    if (clock) clock->end(i);
   };
   const bool has_shared = L.shared_intermediate > 0;
   uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
@@ -410,25 +423,33 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     d.shared_pair_blocks = has_shared ? (d.Is + 4 * kDecodeRowsPerWave - 1) / (4 * kDecodeRowsPerWave) : 0;
     d.max_groups = std::min(A, E);
     if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
-    hipError_t e = launch_decode_block(d, s, marks);
-    stage = 6;  // launch_decode_block recorded marks[0..5]
-    // the shared expert ran inside the router and down kernels, the combine inside the
-    // down kernel: empty stages
-    mark();
-    mark();
+    // kernel-attached events: router | gate/up (shared gate/up, routing, sort inside) |
+    // down (shared down and the combine inside)
+    hipEvent_t kev[6];
+    if (clock) {
+      const int st[3] = {0, 3, 4};
+      for (int i = 0; i < 3; ++i) {
+        clock->used[st[i]] = true;
+        kev[2 * i] = clock->ev[2 * st[i]];
+        kev[2 * i + 1] = clock->ev[2 * st[i] + 1];
+      }
+    }
+    hipError_t e = launch_decode_block(d, s, clock ? kev : nullptr);
     if (e != hipSuccess) return hip_fail(kBlockOp, e);
     return ok();
   }
 
-  mark();
+  begin(0);
   hipError_t e = run_router(L, x, T, logits, s);
-  mark();
+  end(0);
+  begin(1);
   if (e == hipSuccess) e = launch_route_topk(logits, T, E, k, L.normalize_top_k, idx, scores, s);
-  mark();
+  end(1);
+  begin(2);
   if (e == hipSuccess)
     e = launch_sort(idx, A, E, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
                     tile_count, s);
-  mark();
+  end(2);
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
 
   // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / k]
@@ -450,8 +471,9 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   gu.max_tiles = o.max_tiles;
   gu.C = act;
   gu.ldc = I;
+  begin(3);
   e = launch_grouped_gemm(gu, kEpiSwiglu, s);
-  mark();
+  end(3);
 
   GemmArgs dn{};
   dn.A = act;
@@ -467,16 +489,20 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   dn.max_tiles = o.max_tiles;
   dn.C = eout;
   dn.ldc = H;
+  begin(4);
   if (e == hipSuccess) e = launch_grouped_gemm(dn, kEpiPlain, s);
-  mark();
+  end(4);
 
-  if (e == hipSuccess && has_shared)
-    e = run_shared(L, x, T, (uint16_t *)at(o.shared_act), shared_out, z, s);
-  mark();
+  if (has_shared) {
+    begin(5);
+    if (e == hipSuccess) e = run_shared(L, x, T, (uint16_t *)at(o.shared_act), shared_out, z, s);
+    end(5);
+  }
   // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
+  begin(6);
   if (e == hipSuccess)
     e = launch_combine(eout, inverse, scores, T, k, H, A >= 64, shared_out, z, sparse, y, s);
-  mark();
+  end(6);
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
   return ok();
 }
@@ -530,22 +556,23 @@ int astro_moe_block_forward_attributed(const astro_moe_layer *layer, const uint1
                                        int32_t tokens, uint16_t *y, void *workspace,
                                        size_t workspace_bytes, void *stream, float *stage_ms) {
   if (!stage_ms) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "stage time output must be non-null");
-  hipEvent_t marks[ASTRO_MOE_STAGES + 1];
-  for (int i = 0; i <= ASTRO_MOE_STAGES; ++i) {
-    hipError_t e = hipEventCreate(&marks[i]);
+  hipEvent_t ev[2 * ASTRO_MOE_STAGES];
+  for (int i = 0; i < 2 * ASTRO_MOE_STAGES; ++i) {
+    hipError_t e = hipEventCreate(&ev[i]);
     if (e != hipSuccess) {
-      for (int j = 0; j < i; ++j) (void)hipEventDestroy(marks[j]);
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
       return hip_fail(kBlockOp, e);
     }
   }
-  int rc = run_block(layer, x, tokens, y, workspace, workspace_bytes, stream, marks);
-  if (rc == ASTRO_MOE_OK) {
-    hipError_t e = hipEventSynchronize(marks[ASTRO_MOE_STAGES]);
-    for (int i = 0; i < ASTRO_MOE_STAGES && e == hipSuccess; ++i)
-      e = hipEventElapsedTime(&stage_ms[i], marks[i], marks[i + 1]);
-    if (e != hipSuccess) rc = hip_fail(kBlockOp, e);
+  StageClock clock{ev, (hipStream_t)stream, {}};
+  int rc = run_block(layer, x, tokens, y, workspace, workspace_bytes, stream, &clock);
+  hipError_t e = rc == ASTRO_MOE_OK ? hipStreamSynchronize((hipStream_t)stream) : hipSuccess;
+  for (int i = 0; i < ASTRO_MOE_STAGES && rc == ASTRO_MOE_OK && e == hipSuccess; ++i) {
+    stage_ms[i] = 0.0f;
+    if (clock.used[i]) e = hipEventElapsedTime(&stage_ms[i], ev[2 * i], ev[2 * i + 1]);
   }
-  for (int i = 0; i <= ASTRO_MOE_STAGES; ++i) (void)hipEventDestroy(marks[i]);
+  if (rc == ASTRO_MOE_OK && e != hipSuccess) rc = hip_fail(kBlockOp, e);
+  for (int i = 0; i < 2 * ASTRO_MOE_STAGES; ++i) (void)hipEventDestroy(ev[i]);
   return rc == ASTRO_MOE_OK ? ok() : rc;
 }
 

@@ -16,6 +16,8 @@
 #include "kernels.h"
 #include "route_dev.h"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 
 namespace astro {
@@ -511,64 +513,73 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   p.y[(int64_t)t * p.H + h] = (uint16_t)out;
 }
 
+// 256-thread launch; ev (nullable) = {start, stop} events recorded around the kernel itself
+template <typename Kernel>
+void launch_timed(Kernel kernel, dim3 grid, hipStream_t s, const hipEvent_t *ev, const DecodeArgs &a) {
+  if (ev)
+    hipExtLaunchKernelGGL(kernel, grid, dim3(256), 0, s, ev[0], ev[1], 0, a);
+  else
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, a);
+}
+
 template <int BITS, int MT, int NC, int PER>
-void launch_gate_up_per(const DecodeArgs &a, hipStream_t s) {
+void launch_gate_up_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   // x: routed row blocks, or the shared expert's pair blocks and its output-gate block
   const int routed_x = (a.I + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave);
   const int shared_x = a.Is > 0 ? a.shared_pair_blocks + 1 : 0;
-  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, MT, NC, PER>),
-                     dim3(std::max(routed_x, shared_x), a.max_groups + 1), dim3(256), 0, s, a);
+  launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER>, dim3(std::max(routed_x, shared_x), a.max_groups + 1),
+               s, ev, a);
 }
 
 template <int BITS, int MT, int NC>
-void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s) {
+void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   const int per = (a.E + 63) / 64;
-  if (per <= 1) launch_gate_up_per<BITS, MT, NC, 1>(a, s);
-  else if (per <= 2) launch_gate_up_per<BITS, MT, NC, 2>(a, s);
-  else if (per <= 4) launch_gate_up_per<BITS, MT, NC, 4>(a, s);
-  else if (per <= 8) launch_gate_up_per<BITS, MT, NC, 8>(a, s);
-  else launch_gate_up_per<BITS, MT, NC, 16>(a, s);
+  if (per <= 1) launch_gate_up_per<BITS, MT, NC, 1>(a, s, ev);
+  else if (per <= 2) launch_gate_up_per<BITS, MT, NC, 2>(a, s, ev);
+  else if (per <= 4) launch_gate_up_per<BITS, MT, NC, 4>(a, s, ev);
+  else if (per <= 8) launch_gate_up_per<BITS, MT, NC, 8>(a, s, ev);
+  else launch_gate_up_per<BITS, MT, NC, 16>(a, s, ev);
 }
 
 template <int BITS, int NC>
-void launch_down_nc(const DecodeArgs &a, hipStream_t s) {
+void launch_down_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   const dim3 grid(a.H / 4, a.T);
   // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
   if (a.A >= 64)
-    hipLaunchKernelGGL((decode_down_kernel<BITS, NC, true>), grid, dim3(256), 0, s, a);
+    launch_timed(decode_down_kernel<BITS, NC, true>, grid, s, ev, a);
   else
-    hipLaunchKernelGGL((decode_down_kernel<BITS, NC, false>), grid, dim3(256), 0, s, a);
+    launch_timed(decode_down_kernel<BITS, NC, false>, grid, s, ev, a);
 }
 
 template <int BITS, int MT>
-void launch_gate_up_mt(const DecodeArgs &a, hipStream_t s) {
-  if (a.H <= 2048) launch_gate_up_nc<BITS, MT, 1>(a, s);
-  else launch_gate_up_nc<BITS, MT, 2>(a, s);
+void launch_gate_up_mt(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
+  if (a.H <= 2048) launch_gate_up_nc<BITS, MT, 1>(a, s, ev);
+  else launch_gate_up_nc<BITS, MT, 2>(a, s, ev);
 }
 
 template <int BITS>
-void launch_gate_up(const DecodeArgs &a, int mt, hipStream_t s) {
-  if (mt == 1) launch_gate_up_mt<BITS, 1>(a, s);
-  else if (mt == 2) launch_gate_up_mt<BITS, 2>(a, s);
-  else if (mt == 4) launch_gate_up_mt<BITS, 4>(a, s);
-  else launch_gate_up_mt<BITS, 8>(a, s);
+void launch_gate_up(const DecodeArgs &a, int mt, hipStream_t s, const hipEvent_t *ev) {
+  if (mt == 1) launch_gate_up_mt<BITS, 1>(a, s, ev);
+  else if (mt == 2) launch_gate_up_mt<BITS, 2>(a, s, ev);
+  else if (mt == 4) launch_gate_up_mt<BITS, 4>(a, s, ev);
+  else launch_gate_up_mt<BITS, 8>(a, s, ev);
 }
 
 template <int BITS>
-void launch_down(const DecodeArgs &a, hipStream_t s) {
-  if (std::max(a.I, a.Is) <= 512) launch_down_nc<BITS, 1>(a, s);
-  else launch_down_nc<BITS, 2>(a, s);
+void launch_down(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
+  if (std::max(a.I, a.Is) <= 512) launch_down_nc<BITS, 1>(a, s, ev);
+  else launch_down_nc<BITS, 2>(a, s, ev);
 }
 
 template <int MT, int NC>
-void launch_router_nc(const DecodeArgs &a, int blocks, hipStream_t s) {
-  hipLaunchKernelGGL((decode_router_kernel<MT, NC>), dim3(blocks), dim3(256), 0, s, a);
+void launch_router_nc(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
+  launch_timed(decode_router_kernel<MT, NC>, dim3(blocks), s, ev, a);
 }
 
 template <int MT>
-void launch_router(const DecodeArgs &a, int blocks, hipStream_t s) {
-  if (a.H <= 2048) launch_router_nc<MT, 1>(a, blocks, s);
-  else launch_router_nc<MT, 2>(a, blocks, s);
+void launch_router(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
+  if (a.H <= 2048) launch_router_nc<MT, 1>(a, blocks, s, ev);
+  else launch_router_nc<MT, 2>(a, blocks, s, ev);
 }
 
 }  // namespace
@@ -583,35 +594,26 @@ bool decode_supported(const DecodeArgs &a) {
                         a.sg_group >= 32 && a.sz_group >= 32));
 }
 
-hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *marks) {
+hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, const hipEvent_t *kev) {
   const int mt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8;
-  int stage = 0;
-  auto mark = [&]() {
-    if (marks) (void)hipEventRecord(marks[stage++], s);
-  };
+  const hipEvent_t *e1 = kev ? kev : nullptr, *e2 = kev ? kev + 2 : nullptr,
+                   *e3 = kev ? kev + 4 : nullptr;
   // D1: router rows (4 experts per block)
-  const int blocks = a.router_blocks;
-  mark();
-  if (mt == 1) launch_router<1>(a, blocks, s);
-  else if (mt == 2) launch_router<2>(a, blocks, s);
-  else if (mt == 4) launch_router<4>(a, blocks, s);
-  else launch_router<8>(a, blocks, s);
+  if (mt == 1) launch_router<1>(a, a.router_blocks, s, e1);
+  else if (mt == 2) launch_router<2>(a, a.router_blocks, s, e1);
+  else if (mt == 4) launch_router<4>(a, a.router_blocks, s, e1);
+  else launch_router<8>(a, a.router_blocks, s, e1);
   hipError_t e = hipGetLastError();
-  mark();
   if (e != hipSuccess) return e;
-  // routing and sorting run inside the gate/up kernel: their stages are empty here
-  mark();
-  mark();
-  if (a.gu_bits == 8) launch_gate_up<8>(a, mt, s);
-  else launch_gate_up<4>(a, mt, s);
+  // D2: shared gate/up, routing, routed gate/up
+  if (a.gu_bits == 8) launch_gate_up<8>(a, mt, s, e2);
+  else launch_gate_up<4>(a, mt, s, e2);
   e = hipGetLastError();
-  mark();
   if (e != hipSuccess) return e;
-  if (a.dn_bits == 8) launch_down<8>(a, s);
-  else launch_down<4>(a, s);
-  e = hipGetLastError();
-  mark();
-  return e;
+  // D3: down projections and the combine
+  if (a.dn_bits == 8) launch_down<8>(a, s, e3);
+  else launch_down<4>(a, s, e3);
+  return hipGetLastError();
 }
 
 }  // namespace astro

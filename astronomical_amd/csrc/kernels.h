@@ -109,8 +109,8 @@ struct DecodeArgs {
 bool decode_supported(const DecodeArgs &a);
 constexpr int kDecodeRowsPerWave = 1;  // must match kRowsPerWave in decode.hip
 constexpr int kDecodeMaxK = 8;         // experts per token the decode combine unrolls
-// launches the three decode kernels, combine included; marks (nullable) receives 6 stage
-// boundaries (router | route | sort | gate_up | down), the route and sort stages empty
-hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, hipEvent_t *marks);
+// launches the three decode kernels (router | shared gate/up + routing + routed gate/up |
+// down + combine); kev (nullable) = start/stop event pairs recorded around each kernel
+hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, const hipEvent_t *kev);
 
 }  // namespace astro

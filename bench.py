@@ -8,8 +8,12 @@ so the step's ~640 MB of selected pages come from HBM, not the 256 MB Infinity C
 each step is one captured HIP graph.  value = layers * steps / timed seconds.
 
 Also reported: prefill of 2048 tokens (config c2) with per-stage times, the roofline of
-the dominant kernel (per-stage hipEvents over the timed workload), and the CPU oracle
-(C restatement of the reference op graph) timed on a bounded sample on the host cores.
+the dominant decode kernel (its average duration from start/stop events attached to its
+own dispatches over K x L eager calls; HBM traffic per launch from the rocprofv3 counter
+summary profiles/decode_traffic.json when present), and the CPU oracle (C restatement of
+the reference op graph) timed on a bounded sample on the host cores.
+--copy-check first runs a plain 1 GiB device-to-device copy three times: the reference
+dispatch that scales the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu]
 """
@@ -26,6 +30,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+# attributed stage -> decode kernel that carries it (the other stages run inside these)
+DECODE_KERNELS = {"router": "decode_router_kernel", "gate_up": "decode_gate_up_kernel",
+                  "down": "decode_down_kernel"}
 BF16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 
@@ -42,6 +49,8 @@ def parse():
     p.add_argument("--prefill-iters", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--copy-check", action="store_true",
+                   help="run a 1 GiB streaming copy first (counter calibration)")
     return p.parse_args()
 
 
@@ -61,6 +70,15 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_check:
+        # a plain streaming kernel of known traffic: reads 1 GiB, writes 1 GiB
+        a = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            torch.mul(a, 1.0, out=b)
+        torch.cuda.synchronize()
+        del a, b
+        log("copy check: 3 x (1 GiB read + 1 GiB write) elementwise kernel")
     cfg = CF.C1
     nL, K, W = args.layers, args.steps, args.warmup
 
@@ -120,20 +138,35 @@ def main():
     layer_gbs = credited / (ms_per_layer * 1e-3) / 1e9
 
     log(f"decode: {ms_per_layer * 1000:.2f} us/layer")
-    # per-stage device times of the same decode workload (eager, event-bracketed stages)
+    # per-kernel device times of the same decode workload: eager calls of the attributed
+    # entry point, whose decode kernels carry start/stop events on their own dispatches
+    # (hipExtLaunchKernelGGL) on the stream they run on
     stage_acc = {}
-    for s in range(W, W + min(K, 5)):
+    for s in range(W, W + K):
         for l in range(nL):
             _, st = blocks[l].forward_attributed(toks[s, l], out=outs[l], workspace=ws)
             for kname, v in st.items():
                 stage_acc.setdefault(kname, []).append(v)
     stage_ms = {kname: statistics.mean(v) for kname, v in stage_acc.items()}
-    dom = max(("gate_up", "down"), key=lambda s_: stage_ms[s_])
-    # algorithmic bytes of one launch of the dominant kernel at B=1: 8 routed pages
-    H, I, g, b = cfg.hidden, cfg.intermediate, cfg.group_size, cfg.bits
-    per_elem = b / 8 + 4 / g
-    dom_bytes = cfg.top_k * (2 * I * H if dom == "gate_up" else H * I) * per_elem
-    dom_gbs = dom_bytes / (stage_ms[dom] * 1e-3) / 1e9
+    kernel_ms = {DECODE_KERNELS[s_]: stage_ms[s_] for s_ in DECODE_KERNELS}
+    # algorithmic bytes of one launch of each decode kernel at B=1 (weights read once each)
+    H, I, Is, E, kk = cfg.hidden, cfg.intermediate, cfg.shared_intermediate, cfg.experts, cfg.top_k
+    per_elem = cfg.bits / 8 + 4 / cfg.group_size  # codes + bf16 scale and bias per group
+    kernel_bytes = {
+        "decode_router_kernel": E * H * 2,
+        "decode_gate_up_kernel": (kk * 2 * I * H + 2 * Is * H + H) * per_elem,
+        "decode_down_kernel": (kk * H * I + H * Is) * per_elem,
+    }
+    dom = max(kernel_ms, key=lambda k_: kernel_ms[k_])
+    dom_bytes = kernel_bytes[dom]
+    dom_gbs = dom_bytes / (kernel_ms[dom] * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tr = json.load(f).get(dom)
+        if tr:
+            traffic = int(tr["fetch_bytes"] + tr["write_bytes"])
 
     # ---------------------------------------------------------------- prefill 2048 (c2)
     T = 2048
@@ -189,21 +222,22 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"grouped_gemm ({dom}) at decode B=1",
+            "kernel": f"{dom} (decode B=1, c1)",
             "achieved": round(dom_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_launch": int(dom_bytes),
-            "avg_launch_us": round(stage_ms[dom] * 1000, 2),
+            "avg_launch_us": round(kernel_ms[dom] * 1000, 2),
         },
         "layer_roofline": {
             "credited_bytes_per_layer": int(credited),
             "achieved_GBps": round(layer_gbs, 1),
             "frac_of_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
         },
-        "decode_stage_us": {k_: round(v * 1000, 2) for k_, v in stage_ms.items()},
+        "decode_kernel_us": {k_: round(v * 1000, 2) for k_, v in kernel_ms.items()},
+        "decode_kernel_GBps": {k_: round(kernel_bytes[k_] / (v * 1e-3) / 1e9, 1) for k_, v in kernel_ms.items()},
         "prefill": {
             "workload": "c2: c1 shapes, 2048 tokens, sorted path",
             "ms": round(prefill_ms, 4),
@@ -232,8 +266,9 @@ def cpu_baseline(layer_dev, toks, cfg, seconds):
     xs = bf16_to_numpy(toks.reshape(-1, cfg.hidden))
     n = 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds and n < xs.shape[0]:
-        oracle.moe_block_forward(Lh, xs[n:n + 1])
+    while time.perf_counter() - t0 < seconds:
+        i = n % xs.shape[0]
+        oracle.moe_block_forward(Lh, xs[i:i + 1])
         n += 1
     el = time.perf_counter() - t0
     return {"value": round(n / el, 2), "unit": "tokens/s", "cores": cores, "kind": "port",

@@ -131,11 +131,15 @@ int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int
 /*
  * The same forward with per-stage device times, the counterpart of the reference's
  * PerformanceAttribution operation timers (crates/model-serving/src/performance_attribution.rs:1-80,
- * performance_attribution/catalog.rs:54,89-91) — but measuring device time (hipEvents
- * at stage boundaries) rather than graph construction.  stage_ms[ASTRO_MOE_STAGES]
- * receives: router projection, route (softmax/top-k), sort (assignment preparation),
- * gate/up + SwiGLU, down (gathered expert execution), shared expert, combine (weighted
- * reduction).  Synchronises the stream; not for the hot path.
+ * performance_attribution/catalog.rs:54,89-91) — but measuring device time rather than
+ * graph construction.  stage_ms[ASTRO_MOE_STAGES] receives: router projection, route
+ * (softmax/top-k), sort (assignment preparation), gate/up + SwiGLU, down (gathered expert
+ * execution), shared expert, combine (weighted reduction).  A stage that is one kernel is
+ * timed by events attached to that kernel's dispatch; other stages by event records around
+ * their launches.  The decode path (tokens * top_k <= 64) runs three kernels and reports
+ * them as router, gate/up (which also runs the shared expert's gate/up, the routing and
+ * the sort) and down (which also runs the shared expert's down projection and the
+ * combine); its other stages read 0.  Synchronises the stream; not for the hot path.
  */
 #define ASTRO_MOE_STAGES 7
 int astro_moe_block_forward_attributed(const astro_moe_layer *layer, const uint16_t *x,

@@ -309,6 +309,19 @@ def test_fused_and_separate_gate_up_are_bit_identical(ops):
     assert np.array_equal(_np(fused(x)), _np(sep(x)))
 
 
+def test_attributed_forward_matches_forward(ops, c1_layer):
+    """The attributed entry point computes the same bits and reports the stages it ran:
+    three kernels on the decode path, every stage on the sorted path."""
+    blk = ops.MoeBlock(_device_layer(ops, c1_layer))
+    for T, expect in ((1, {"router", "gate_up", "down"}), (128, set(ops._lib.STAGES))):
+        x = _dev_bf16(S.make_tokens(CF.C1, T))
+        y = _np(blk(x))
+        y2, st = blk.forward_attributed(x)
+        assert np.array_equal(_np(y2), y)
+        assert {k for k, v in st.items() if v > 0} == expect, (T, st)
+        assert all(0 <= v < 50 for v in st.values()), st
+
+
 def test_empty_token_batch(ops):
     L = S.make_layer(CF.C0)
     blk = ops.MoeBlock(_device_layer(ops, L))
