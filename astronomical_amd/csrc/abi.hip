@@ -107,7 +107,7 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Layout {
   size_t logits, idx, scores, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
-      tile_count, act, eout, sparse, shared_act, shared_out, z, groups, total;
+      tile_count, act, eout, sparse, shared_act, shared_out, z, groups, sort_scratch, total;
   int max_tiles;
   bool decode;     // wavefront-GEMV path: act / eout hold A routed rows then T shared rows
   int64_t act_ld;  // row length of act
@@ -157,6 +157,7 @@ Layout block_layout(const astro_moe_layer &L, int T) {
     o.tile_expert = take((size_t)o.max_tiles * 4);
     o.tile_row0 = take((size_t)o.max_tiles * 4);
     o.tile_count = take(4);
+    o.sort_scratch = take(sort_scratch_bytes((int)A, (int)E));
     o.act_ld = L.intermediate;
     o.act = take(A * (size_t)L.intermediate * 2);
     o.eout = take(A * (size_t)L.hidden * 2);
@@ -251,37 +252,48 @@ hipError_t run_router(const astro_moe_layer &L, const uint16_t *x, int T, uint16
   return launch_grouped_gemm(g, L.router_bias ? kEpiBias : kEpiPlain, s);
 }
 
-// shared expert: act = swiglu(gate(x), up(x)); out = down(act); z = shared_expert_gate(x)
-hipError_t run_shared(const astro_moe_layer &L, const uint16_t *x, int T, uint16_t *act,
-                      uint16_t *out, uint16_t *z, hipStream_t s) {
-  GemmArgs g{};
-  g.A = x;
-  g.lda = L.hidden;
-  g.a_div = 1;
-  g.K = L.hidden;
-  g.N = L.shared_intermediate;
-  g.M = T;
-  set_weights(g, L.shared_gate, &L.shared_up, 0);
-  g.w_expert_stride = g.sb_expert_stride = 0;
-  g.C = act;
-  g.ldc = L.shared_intermediate;
-  hipError_t e = launch_grouped_gemm(g, kEpiSwiglu, s);
-  if (e != hipSuccess) return e;
-  GemmArgs d{};
-  d.A = act;
-  d.lda = L.shared_intermediate;
-  d.a_div = 1;
-  d.K = L.shared_intermediate;
-  d.N = L.hidden;
-  d.M = T;
-  set_weights(d, L.shared_down, nullptr, 0);
-  d.C = out;
-  d.ldc = L.hidden;
-  e = launch_grouped_gemm(d, kEpiPlain, s);
-  if (e != hipSuccess) return e;
+// shared expert problems: act = swiglu(gate(x), up(x)) (gu); out = down(act) (dn)
+void shared_gemm_args(const astro_moe_layer &L, const uint16_t *x, int T, uint16_t *act,
+                      uint16_t *out, GemmArgs &gu, GemmArgs &dn) {
+  gu = GemmArgs{};
+  gu.A = x;
+  gu.lda = L.hidden;
+  gu.a_div = 1;
+  gu.K = L.hidden;
+  gu.N = L.shared_intermediate;
+  gu.M = T;
+  set_weights(gu, L.shared_gate, &L.shared_up, 0);
+  gu.w_expert_stride = gu.sb_expert_stride = 0;
+  gu.C = act;
+  gu.ldc = L.shared_intermediate;
+  dn = GemmArgs{};
+  dn.A = act;
+  dn.lda = L.shared_intermediate;
+  dn.a_div = 1;
+  dn.K = L.shared_intermediate;
+  dn.N = L.hidden;
+  dn.M = T;
+  set_weights(dn, L.shared_down, nullptr, 0);
+  dn.C = out;
+  dn.ldc = L.hidden;
+}
+
+hipError_t run_shared_gate(const astro_moe_layer &L, const uint16_t *x, int T, uint16_t *z,
+                           hipStream_t s) {
   const astro_moe_affine &zg = L.shared_expert_gate;
   return launch_qgemv_rows(x, T, L.hidden, zg.w, zg.scales, zg.biases, 1, zg.bits, zg.group_size,
                            z, s);
+}
+
+// shared expert: act = swiglu(gate(x), up(x)); out = down(act); z = shared_expert_gate(x)
+hipError_t run_shared(const astro_moe_layer &L, const uint16_t *x, int T, uint16_t *act,
+                      uint16_t *out, uint16_t *z, hipStream_t s) {
+  GemmArgs gu, dn;
+  shared_gemm_args(L, x, T, act, out, gu, dn);
+  hipError_t e = launch_grouped_gemm(gu, kEpiSwiglu, s);
+  if (e == hipSuccess) e = launch_grouped_gemm(dn, kEpiPlain, s);
+  if (e == hipSuccess) e = run_shared_gate(L, x, T, z, s);
+  return e;
 }
 
 // Per-stage device times for the attributed entry point: a start and a stop event per
@@ -448,7 +460,7 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   begin(2);
   if (e == hipSuccess)
     e = launch_sort(idx, A, E, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
-                    tile_count, s);
+                    tile_count, (uint32_t *)at(o.sort_scratch), s);
   end(2);
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
 
@@ -471,8 +483,12 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   gu.max_tiles = o.max_tiles;
   gu.C = act;
   gu.ldc = I;
+  // the shared expert's gate/up and down run in the same launches as the routed ones
+  GemmArgs sgu, sdn;
+  if (has_shared)
+    shared_gemm_args(L, x, T, (uint16_t *)at(o.shared_act), shared_out, sgu, sdn);
   begin(3);
-  e = launch_grouped_gemm(gu, kEpiSwiglu, s);
+  e = launch_grouped_gemm2(gu, has_shared ? &sgu : nullptr, kEpiSwiglu, s);
   end(3);
 
   GemmArgs dn{};
@@ -490,12 +506,12 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   dn.C = eout;
   dn.ldc = H;
   begin(4);
-  if (e == hipSuccess) e = launch_grouped_gemm(dn, kEpiPlain, s);
+  if (e == hipSuccess) e = launch_grouped_gemm2(dn, has_shared ? &sdn : nullptr, kEpiPlain, s);
   end(4);
 
   if (has_shared) {
     begin(5);
-    if (e == hipSuccess) e = run_shared(L, x, T, (uint16_t *)at(o.shared_act), shared_out, z, s);
+    if (e == hipSuccess) e = run_shared_gate(L, x, T, z, s);
     end(5);
   }
   // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
@@ -605,7 +621,8 @@ int astro_moe_route_topk(const uint16_t *logits, int32_t tokens, int32_t experts
 
 static size_t sort_ws_bytes(int A, int E) {
   const int mt = sort_max_tiles(A, E);
-  return align_up(((size_t)E + 2) * 4) + 2 * align_up((size_t)mt * 4) + align_up(4);
+  return align_up(((size_t)E + 2) * 4) + 2 * align_up((size_t)mt * 4) + align_up(4) +
+         align_up(sort_scratch_bytes(A, E));
 }
 
 int astro_moe_sort_workspace_bytes(int32_t assignments, int32_t experts, size_t *bytes) {
@@ -632,8 +649,9 @@ int astro_moe_sort_assignments(const uint32_t *ids, int32_t assignments, int32_t
   uint32_t *te = (uint32_t *)(ws + align_up(((size_t)experts + 2) * 4));
   uint32_t *tr = (uint32_t *)((char *)te + align_up((size_t)mt * 4));
   uint32_t *tc = (uint32_t *)((char *)tr + align_up((size_t)mt * 4));
+  uint32_t *scr = (uint32_t *)((char *)tc + align_up(4));
   hipError_t e = launch_sort(ids, assignments, experts, sorted_order, inverse_order, sorted_ids,
-                             off, te, tr, tc, s);
+                             off, te, tr, tc, scr, s);
   if (e == hipSuccess && expert_offsets)
     e = hipMemcpyAsync(expert_offsets, off, ((size_t)experts + 1) * 4, hipMemcpyDeviceToDevice, s);
   return e == hipSuccess ? ok() : hip_fail(kSortOp, e);
@@ -686,7 +704,8 @@ int astro_moe_gather_qmm(const uint16_t *x, const uint32_t *x_rows, int32_t rows
   uint32_t *te = (uint32_t *)(sw + align_up(((size_t)E + 2) * 4));
   uint32_t *tr = (uint32_t *)((char *)te + align_up((size_t)mt * 4));
   uint32_t *tc = (uint32_t *)((char *)tr + align_up((size_t)mt * 4));
-  hipError_t e = launch_sort(ids, rows, E, so, inv, sid, off, te, tr, tc, s);
+  uint32_t *scr = (uint32_t *)((char *)tc + align_up(4));
+  hipError_t e = launch_sort(ids, rows, E, so, inv, sid, off, te, tr, tc, scr, s);
   if (e != hipSuccess) return hip_fail(kGatherOp, e);
   GemmArgs g{};
   g.A = x;

@@ -15,6 +15,8 @@
 #include "common.h"
 #include "kernels.h"
 
+#include <algorithm>
+
 namespace astro {
 
 namespace {
@@ -104,24 +106,39 @@ __device__ __forceinline__ void store_b(uint16_t *dst, const BRegs &r, bool vali
   d[3] = out[3];
 }
 
-template <int KIND, int EPI, bool GROUPED>
-__global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs p) {
+// Tile of the launch: blocks x < split belong to problem a, the rest to problem b (a
+// second GEMM fused into the same launch, e.g. the shared expert next to the routed
+// experts).  A problem with a tile table is grouped: x indexes its tiles; otherwise row
+// tiles are consecutive.  Returns false when the block has no work.  The problem is
+// selected by value: taking the address of a kernel argument would copy both to scratch.
+__device__ __forceinline__ bool gemm_tile(const GemmArgs &p, bool second, int split, int nblocks,
+                                          int &expert, int &row0, int &m_valid) {
+  if ((int)blockIdx.y >= nblocks) return false;
+  const int x = second ? (int)blockIdx.x - split : (int)blockIdx.x;
+  expert = 0;
+  if (p.tile_expert) {
+    if (x >= (int)*p.tile_count) return false;
+    expert = (int)p.tile_expert[x];
+    row0 = (int)p.tile_row0[x];
+    m_valid = min(BM, (int)p.expert_offsets[expert + 1] - row0);
+  } else {
+    row0 = x * BM;
+    m_valid = min(BM, p.M - row0);
+  }
+  return m_valid > 0;
+}
+
+template <int KIND, int EPI>
+__global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, const GemmArgs pb,
+                                                           int split, int nba, int nbb) {
   __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDSP];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[BR * LDSP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  int expert = 0, row0, m_valid;
-  if (GROUPED) {
-    const int tile = blockIdx.x;
-    if (tile >= (int)*p.tile_count) return;
-    expert = (int)p.tile_expert[tile];
-    row0 = (int)p.tile_row0[tile];
-    m_valid = min(BM, (int)p.expert_offsets[expert + 1] - row0);
-  } else {
-    row0 = blockIdx.x * BM;
-    m_valid = min(BM, p.M - row0);
-  }
-  if (m_valid <= 0) return;
+  const bool second = (int)blockIdx.x >= split;
+  const GemmArgs p = second ? pb : pa;
+  int expert, row0, m_valid;
+  if (!gemm_tile(p, second, split, second ? nbb : nba, expert, row0, m_valid)) return;
   const int ntile = blockIdx.y;
 
   // ---- per-thread weight row (load stage): row r = tid/2, inputs 32*half.. of a K step
@@ -247,36 +264,373 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs p) {
   }
 }
 
-template <int KIND, bool GROUPED>
-hipError_t launch_kind(const GemmArgs &a, int epi, hipStream_t s) {
-  const int ntiles = epi == kEpiSwiglu ? (a.N + 63) / 64 : (a.N + BR - 1) / BR;
-  int mt = GROUPED ? a.max_tiles : (a.M + BM - 1) / BM;
-  if (mt <= 0 || ntiles <= 0) return hipSuccess;
-  // all column tiles of one row tile land on the same XCD (blocks are dealt to the 8
-  // XCDs round-robin by linear id) when the row-tile count is a multiple of 8
-  mt = (mt + 7) & ~7;
-  dim3 grid(mt, ntiles), block(256);
+template <int KIND>
+hipError_t launch_kind(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_t s) {
+  auto shape = [&](const GemmArgs &g, int &mt, int &nb) {
+    nb = epi == kEpiSwiglu ? (g.N + 63) / 64 : (g.N + BR - 1) / BR;
+    mt = g.tile_expert ? g.max_tiles : (g.M + BM - 1) / BM;
+    // all column tiles of one row tile land on the same XCD (blocks are dealt to the 8
+    // XCDs round-robin by linear id) when the row-tile counts are multiples of 8
+    mt = mt > 0 && nb > 0 ? (mt + 7) & ~7 : 0;
+  };
+  int mta, nba, mtb = 0, nbb = 0;
+  shape(a, mta, nba);
+  if (b) shape(*b, mtb, nbb);
+  if (mta + mtb == 0) return hipSuccess;
+  const GemmArgs &bb = b ? *b : a;
+  dim3 grid(mta + mtb, std::max(nba, nbb)), block(256);
   if (epi == kEpiSwiglu)
-    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiSwiglu, GROUPED>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiSwiglu>), grid, block, 0, s, a, bb, mta, nba, nbb);
   else if (epi == kEpiBias)
-    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiBias, GROUPED>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiBias>), grid, block, 0, s, a, bb, mta, nba, nbb);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiPlain, GROUPED>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((grouped_gemm_kernel<KIND, kEpiPlain>), grid, block, 0, s, a, bb, mta, nba, nbb);
   return hipGetLastError();
 }
 
-template <int KIND>
-hipError_t launch_kind(const GemmArgs &a, int epi, hipStream_t s) {
-  return a.tile_expert ? launch_kind<KIND, true>(a, epi, s) : launch_kind<KIND, false>(a, epi, s);
+// Workgroup barrier without the memory fence of __syncthreads (whose release would wait for
+// every outstanding global->LDS load).  Each wave first waits for its own LDS accesses
+// (lgkmcnt 0), so its LDS stores are visible and its LDS reads are done when it reaches the
+// barrier; the async loads are covered by wait_vmcnt_le before it.  The asm statements
+// also stop the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(n) with expcnt and lgkmcnt at their maxima (no wait on them); n is a
+// compile-time constant at every call, so the switch folds to one instruction.
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+  switch (n) {
+#define ASTRO_WAITVM(N) \
+  case N:               \
+    __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | 0x0f70); \
+    break;
+#define ASTRO_WAITVM8(B) ASTRO_WAITVM(B) ASTRO_WAITVM(B + 1) ASTRO_WAITVM(B + 2) ASTRO_WAITVM(B + 3) \
+  ASTRO_WAITVM(B + 4) ASTRO_WAITVM(B + 5) ASTRO_WAITVM(B + 6) ASTRO_WAITVM(B + 7)
+    ASTRO_WAITVM8(0) ASTRO_WAITVM8(8) ASTRO_WAITVM8(16) ASTRO_WAITVM8(24)
+    ASTRO_WAITVM8(32) ASTRO_WAITVM8(40) ASTRO_WAITVM8(48) ASTRO_WAITVM8(56)
+#undef ASTRO_WAITVM8
+#undef ASTRO_WAITVM
+    default:
+      __builtin_amdgcn_s_waitcnt(0x0f70);
+      break;
+  }
+}
+
+// 8 codes of one word (4-bit: 8 nibbles, LSB first) -> 8 bf16 in input order.  The
+// nibble masks go through asm so that the compiler keeps them as one AND each and converts
+// every byte with one v_cvt_f32_ubyte{0..3} (it would otherwise re-derive each nibble
+// with a bit-field extract first).
+__device__ __forceinline__ u32x4 dequant8_q4(uint32_t w, float s, float b) {
+  uint32_t lo, hi;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi) : "v"(w >> 4));
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float q0 = (float)((lo >> (8 * i)) & 255u), q1 = (float)((hi >> (8 * i)) & 255u);
+    o[i] = pack_bf2_hw(__builtin_fmaf(s, q0, b), __builtin_fmaf(s, q1, b));
+  }
+  return o;
+}
+
+// ---------------------------------------------------------------- warp-specialised GEMM
+//
+// 4-bit affine weights, K a multiple of 64, groups of >= 32 inputs (an even number per
+// row).  A workgroup of 8 waves owns one tile of up to 128 rows of one expert and 256
+// weight rows (plain: 256 output columns; SwiGLU: 128 activated columns = 128 gate + 128
+// up rows), stepping K by 64.  The waves specialise:
+//   - producers (waves 0-3) issue the direct global->LDS loads of the activation tile, the
+//     codes and the scales / biases two steps ahead, and turn step k+1's codes into a bf16
+//     weight tile in LDS (thread t: weight row t, 64 inputs);
+//   - consumers (waves 4-7) run the MFMAs of step k: wave 4 + w owns weight rows
+//     64 w .. +64 and every row block of the tile.
+// One s_barrier per step separates the roles' uses of the rings (A, codes, scales: 3 slots;
+// bf16 weights: 2 slots), so each SIMD runs a producer's dequantisation next to a
+// consumer's MFMAs.  Producers wait for their own loads with explicit vmcnt counts; no
+// register loads happen inside the loop, so the compiler adds no waits of its own.
+// LDS rows are 128 B (64 bf16) with 16-B chunk c of row r at position c ^ ((r >> 1) & 7),
+// which spreads the 16 rows of an MFMA fragment over all 64 banks.
+constexpr int WK = 64;                         // K step
+constexpr int WNB = 256;                       // weight rows per workgroup
+constexpr int WA_SLOT = 128 * WK * 2;          // 16 KB: activation tile
+constexpr int WC_SLOT = WNB * WK / 2;          // 8 KB: 4-bit codes
+constexpr int WS_SLOT = 2 * WNB * 4;           // 2 KB: one dword of scales, one of biases
+constexpr int WB_SLOT = WNB * WK * 2;          // 32 KB: bf16 weight tile
+constexpr int WOFF_C = 3 * WA_SLOT, WOFF_S = WOFF_C + 3 * WC_SLOT, WOFF_B = WOFF_S + 3 * WS_SLOT;
+constexpr int kWsLds = WOFF_B + 2 * WB_SLOT;   // 142 KB
+
+__device__ __forceinline__ int wswz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+// consumer: MFMAs of one K step over 4 column blocks and row blocks 0..3, plus 4..7 when the
+// tile has more than 64 rows (one uniform branch per sub-step)
+__device__ __forceinline__ void ws_mfma_step(const char *as, const char *bs, int cw, int lane,
+                                             bool full, f32x4 (&acc)[8][4]) {
+  const int c16 = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    bf16x8 bf[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int n = cw * 64 + f * 16 + c16;
+      bf[f] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(bs + n * 128 + 16 * wswz(n, 4 * j + kq)));
+    }
+    auto rows = [&](int rb) {
+      const int r = rb * 16 + c16;
+      const bf16x8 af = __builtin_bit_cast(bf16x8, *(const u32x4 *)(as + r * 128 + 16 * wswz(r, 4 * j + kq)));
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        acc[rb][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[f], acc[rb][f], 0, 0, 0);
+    };
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) rows(rb);
+    if (full) {
+#pragma unroll
+      for (int rb = 4; rb < 8; ++rb) rows(rb);
+    }
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(512) void ws_gemm_kernel(const GemmArgs pa, const GemmArgs pb, int split,
+                                                      int nba, int nbb) {
+  extern __shared__ __attribute__((aligned(16))) char ws_lds[];
+  typedef __attribute__((address_space(3))) void lds_void;
+  const bool second = (int)blockIdx.x >= split;
+  const GemmArgs p = second ? pb : pa;
+  int expert, row0, m_valid;
+  if (!gemm_tile(p, second, split, second ? nbb : nba, expert, row0, m_valid)) return;
+  const int nblk = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nk = p.K / WK;
+  const bool producer = wave < 4;
+
+  if (producer) {
+    // ---- this thread's weight row t = tid (0..255)
+    const int t = tid;
+    int n;
+    bool upper = false;
+    if (EPI == kEpiSwiglu) {
+      // consumer block t / 64 holds 32 gate rows then the 32 up rows of the same columns
+      upper = (t & 63) >= 32;
+      n = nblk * (WNB / 2) + (t >> 6) * 32 + (t & 31);
+    } else {
+      n = nblk * WNB + t;
+    }
+    const int nc = n < p.N ? n : p.N - 1;  // rows past N load a valid row; never stored
+    const uint32_t *wrow = (upper ? p.w1 : p.w0) + (int64_t)expert * p.w_expert_stride + (int64_t)nc * p.w_row_stride;
+    const int64_t so = (int64_t)expert * p.sb_expert_stride + (int64_t)nc * p.sb_row_stride;
+    const uint16_t *srow = (upper ? p.s1 : p.s0) + so;
+    const uint16_t *brow = (upper ? p.b1 : p.b0) + so;
+    // ---- A rows: load v of producer wave w fills rows (v * 4 + w) * 8 + lane / 8, position
+    // lane % 8 (holding K chunk wswz(row, lane % 8))
+    const uint16_t *asrc[4];
+    {
+      int src[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = (v * 4 + wave) * 8 + (lane >> 3);
+        src[v] = row0 + (r < m_valid ? r : 0);
+      }
+      if (p.a_rows) {
+        uint32_t tt[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tt[v] = p.a_rows[src[v]];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) src[v] = (int)(tt[v] / (uint32_t)p.a_div);
+      }
+      if (p.a_rows2) {
+        uint32_t tt[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tt[v] = p.a_rows2[src[v]];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) src[v] = (int)tt[v];
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = (v * 4 + wave) * 8 + (lane >> 3);
+        asrc[v] = p.A + (int64_t)src[v] * p.lda + 8 * wswz(r, lane & 7);
+      }
+    }
+    // group of each half of the step (32 inputs), as dword index / half within the dword
+    auto issue_a = [&](int k) {  // 4 loads
+      const int kc = k < nk ? k : nk - 1;
+      char *base = ws_lds + (k % 3) * WA_SLOT;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        __builtin_amdgcn_global_load_lds((const void *)(asrc[v] + kc * WK),
+                                         (lds_void *)(base + (v * 4 + wave) * 1024), 16, 0, 0);
+    };
+    auto issue_c = [&](int k) {  // 4 loads: codes (2 x 16 B), the scale and the bias dword
+      const int kc = k < nk ? k : nk - 1;
+      const int k0 = kc * WK;
+      char *cb = ws_lds + WOFF_C + (k % 3) * WC_SLOT;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        __builtin_amdgcn_global_load_lds((const void *)(wrow + k0 / 8 + 4 * h),
+                                         (lds_void *)(cb + (h * 4 + wave) * 1024), 16, 0, 0);
+      const int gd = (k0 / p.group) & ~1;  // dword holding the step's first group
+      char *sb = ws_lds + WOFF_S + (k % 3) * WS_SLOT;
+      __builtin_amdgcn_global_load_lds((const void *)(srow + gd), (lds_void *)(sb + wave * 256), 4, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(brow + gd), (lds_void *)(sb + 1024 + wave * 256), 4, 0, 0);
+    };
+    auto dequant = [&](int k) {  // codes of step k -> bf16 slot k % 2
+      const char *cb = ws_lds + WOFF_C + (k % 3) * WC_SLOT;
+      const char *sb = ws_lds + WOFF_S + (k % 3) * WS_SLOT;
+      const uint32_t sw = *(const uint32_t *)(sb + wave * 256 + lane * 4);
+      const uint32_t bw = *(const uint32_t *)(sb + 1024 + wave * 256 + lane * 4);
+      const int k0 = k * WK;
+      char *bs = ws_lds + WOFF_B + (k & 1) * WB_SLOT;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 q = *(const u32x4 *)(cb + (h * 4 + wave) * 1024 + lane * 16);
+        // group of inputs k0 + 32 h .. +32, relative to the dword's first group
+        const int gi = (k0 + 32 * h) / p.group - ((k0 / p.group) & ~1);
+        const float sc = gi ? bf_hi(sw) : bf_lo(sw);
+        const float bi = gi ? bf_hi(bw) : bf_lo(bw);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int c = h * 4 + w;  // 16-B chunk of the row: inputs 8c .. 8c+7
+          *(u32x4 *)(bs + t * 128 + 16 * wswz(t, c)) = dequant8_q4(q[w], sc, bi);
+        }
+      }
+    };
+    constexpr int NA = 4, NC = 4;
+    // prologue: codes 0, then [A 0, codes 1], [A 1, codes 2]
+    issue_c(0);
+    issue_a(0);
+    issue_c(1);
+    issue_a(1);
+    issue_c(2);
+    wait_vmcnt_le(2 * (NA + NC));  // codes 0
+    dequant(0);
+    wait_vmcnt_le(NA + 2 * NC);    // A 0
+    ring_barrier();
+    for (int k = 0; k < nk; ++k) {
+      // step k: the consumers compute step k
+      wait_vmcnt_le(NA + NC);       // codes k + 1
+      if (k + 1 < nk) dequant(k + 1);
+      issue_a(k + 2);
+      issue_c(k + 3);
+      wait_vmcnt_le(NA + 2 * NC);   // A k + 1
+      ring_barrier();
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // drain the clamped trailing loads
+    return;
+  }
+
+  // ---- consumers
+  const int cw = wave - 4;
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[rb][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  ring_barrier();  // step 0's A and weights are ready
+  const bool small = m_valid <= 64;
+  for (int k = 0; k < nk; ++k) {
+    const char *as = ws_lds + (k % 3) * WA_SLOT;
+    const char *bs = ws_lds + WOFF_B + (k & 1) * WB_SLOT;
+    ws_mfma_step(as, bs, cw, lane, !small, acc);
+    ring_barrier();
+  }
+
+  // ---- epilogue: lane holds column (lane & 15) of each block, rows 4 (lane >> 4) + i
+  const int c16 = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int rb = 0; rb < 8; ++rb) {
+    if (small && rb >= 4) break;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb * 16 + kq * 4 + i;
+      if (r >= m_valid) continue;
+      const int gr = row0 + r;
+      const int dst = p.c_rows ? (int)p.c_rows[gr] : gr;
+      uint16_t *crow = p.C + (int64_t)dst * p.ldc;
+      if (EPI == kEpiSwiglu) {
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const int col = nblk * (WNB / 2) + cw * 32 + f * 16 + c16;
+          if (col < p.N) {
+            const float g = round_bf(acc[rb][f][i]);
+            const float u = round_bf(acc[rb][f + 2][i]);
+            crow[col] = (uint16_t)swiglu_bf(g, u);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          const int col = nblk * WNB + cw * 64 + f * 16 + c16;
+          if (col < p.N) {
+            float v = acc[rb][f][i];
+            if (EPI == kEpiBias) v = round_bf(v) + bf2f(p.bias[col]);
+            crow[col] = (uint16_t)f2bf(v);
+          }
+        }
+      }
+    }
+  }
+}
+
+
+hipError_t launch_ws(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_t s) {
+  auto shape = [&](const GemmArgs &g, int &mt, int &nb) {
+    nb = epi == kEpiSwiglu ? (g.N + WNB / 2 - 1) / (WNB / 2) : (g.N + WNB - 1) / WNB;
+    mt = g.tile_expert ? g.max_tiles : (g.M + BM - 1) / BM;
+    mt = mt > 0 && nb > 0 ? (mt + 7) & ~7 : 0;  // one XCD per row tile (see launch_kind)
+  };
+  int mta, nba, mtb = 0, nbb = 0;
+  shape(a, mta, nba);
+  if (b) shape(*b, mtb, nbb);
+  if (mta + mtb == 0) return hipSuccess;
+  const GemmArgs &bb = b ? *b : a;
+  dim3 grid(mta + mtb, std::max(nba, nbb)), block(512);
+  static bool raised[3] = {false, false, false};  // > 64 KB of LDS is an opt-in per kernel
+  auto launch = [&](auto kernel, int which) {
+    if (!raised[which]) {
+      const hipError_t e = hipFuncSetAttribute((const void *)kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kWsLds);
+      if (e != hipSuccess) return e;
+      raised[which] = true;
+    }
+    hipLaunchKernelGGL(kernel, grid, block, kWsLds, s, a, bb, mta, nba, nbb);
+    return hipGetLastError();
+  };
+  if (epi == kEpiSwiglu) return launch(ws_gemm_kernel<kEpiSwiglu>, 0);
+  if (epi == kEpiBias) return launch(ws_gemm_kernel<kEpiBias>, 1);
+  return launch(ws_gemm_kernel<kEpiPlain>, 2);
+}
+
+bool use_ws(const GemmArgs &a) {
+  // 4-bit weights with K steps of 64 and an even number of groups of >= 32 inputs per row
+  // (one dword of scales per step stays 4-byte aligned); K >= 1024: with fewer K steps its
+  // two-step prefetch ramp outweighs the gain
+  return a.bkind == kBQ4 && a.K % WK == 0 && a.K >= 1024 && a.group >= 32 && (a.K / a.group) % 2 == 0;
 }
 
 }  // namespace
 
 hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s) {
+  return launch_grouped_gemm2(a, nullptr, epilogue, s);
+}
+
+bool gemm_fusable(const GemmArgs &a, const GemmArgs &b) {
+  return a.bkind == b.bkind && use_ws(a) == use_ws(b);
+}
+
+hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilogue, hipStream_t s) {
+  if (b && !gemm_fusable(a, *b)) {
+    const hipError_t e = launch_grouped_gemm2(a, nullptr, epilogue, s);
+    return e == hipSuccess ? launch_grouped_gemm2(*b, nullptr, epilogue, s) : e;
+  }
+  if (use_ws(a)) return launch_ws(a, b, epilogue, s);
   switch (a.bkind) {
-    case kBQ4: return launch_kind<kBQ4>(a, epilogue, s);
-    case kBQ8: return launch_kind<kBQ8>(a, epilogue, s);
-    default: return launch_kind<kBDense>(a, epilogue, s);
+    case kBQ4: return launch_kind<kBQ4>(a, b, epilogue, s);
+    case kBQ8: return launch_kind<kBQ8>(a, b, epilogue, s);
+    default: return launch_kind<kBDense>(a, b, epilogue, s);
   }
 }
 

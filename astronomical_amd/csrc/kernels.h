@@ -49,6 +49,9 @@ struct GemmArgs {
 };
 
 hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s);
+// a and, when b is non-null, a second problem b with the same epilogue in one launch (its
+// tiles follow a's); problems the same kernel cannot serve are launched one after the other
+hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilogue, hipStream_t s);
 
 hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
                              uint32_t *idx, uint16_t *scores, hipStream_t s);
@@ -56,10 +59,12 @@ hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int no
 // counting sort of assignment ids by expert (stable), plus the grouped-GEMM tile table
 // (tiles of kGemmBM rows).  offsets has E+2 entries (ids >= E land in a trailing
 // bucket that no tile covers).
+// scratch: sort_scratch_bytes(A, E) bytes (per-chunk histograms and local ranks)
 hipError_t launch_sort(const uint32_t *ids, int A, int E, uint32_t *sorted_order,
                        uint32_t *inverse_order, uint32_t *sorted_ids, uint32_t *offsets,
                        uint32_t *tile_expert, uint32_t *tile_row0, uint32_t *tile_count,
-                       hipStream_t s);
+                       uint32_t *scratch, hipStream_t s);
+size_t sort_scratch_bytes(int A, int E);
 int sort_max_tiles(int A, int E);
 
 // out[t] = bf16( x[t] . deq(W row n) ) for a few output rows (wave per (token, row)).

@@ -26,101 +26,138 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restr
   }
 }
 
-constexpr int kSortThreads = 1024;
+constexpr int kChunk = 1024;  // assignments per rank / scatter workgroup (16 waves)
 
-// Histogram of expert ids (ids >= E counted in bucket E), exclusive scan -> offsets
-// [E+2], and the tile table: tiles of kGemmBM rows, experts in ascending order.
-__global__ __launch_bounds__(kSortThreads) void sort_count_kernel(
-    const uint32_t *__restrict__ ids, int A, int E, uint32_t *__restrict__ offsets,
+// Stable counting sort in three launches.
+// rank: each workgroup takes kChunk consecutive assignments; every wave ranks its 64 ids
+// (number of earlier lanes with the same bucket, from 64 readlanes) and records, per
+// bucket, its count; the workgroup then turns those into chunk-local ranks (earlier waves'
+// counts + the in-wave rank) and writes the chunk's bucket histogram.
+__global__ __launch_bounds__(kChunk) void sort_rank_kernel(const uint32_t *__restrict__ ids, int A,
+                                                           int E, uint32_t *__restrict__ hist,
+                                                           uint32_t *__restrict__ local_rank) {
+  extern __shared__ uint16_t wcnt[];  // [16 waves][E + 1] (a wave counts at most 64)
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int nb = E + 1;
+  for (int i = threadIdx.x; i < 16 * nb; i += kChunk) wcnt[i] = 0;
+  __syncthreads();
+  const int a = blockIdx.x * kChunk + threadIdx.x;
+  const bool valid = a < A;
+  const uint32_t id = valid ? ids[a] : 0u;
+  const uint32_t b = !valid ? 0xffffffffu : id < (uint32_t)E ? id : (uint32_t)E;
+  uint32_t before = 0, after = 0;
+#pragma unroll 16
+  for (int l = 0; l < 64; ++l) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)b, l);
+    before += (o == b) & (l < lane);
+    after += (o == b) & (l > lane);
+  }
+  if (valid && after == 0) wcnt[w * nb + b] = (uint16_t)(before + 1);  // this lane closes its bucket
+  __syncthreads();
+  if (valid) {
+    uint32_t r = before;
+    for (int v = 0; v < w; ++v) r += wcnt[v * nb + b];
+    local_rank[a] = r;
+  }
+  for (int e = threadIdx.x; e < nb; e += kChunk) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) c += wcnt[v * nb + e];
+    hist[(size_t)blockIdx.x * nb + e] = c;
+  }
+}
+
+// scan: one workgroup.  offsets[e] = sum of earlier buckets (E + 2 entries), base of
+// (chunk, bucket) = offsets[bucket] + that bucket's count in earlier chunks (in place in
+// hist), and the tile table (tiles of kGemmBM rows, experts ascending).
+constexpr int kScanThreads = 1024;
+__global__ __launch_bounds__(kScanThreads) void sort_scan_kernel(
+    uint32_t *__restrict__ hist, int nchunks, int A, int E, uint32_t *__restrict__ offsets,
     uint32_t *__restrict__ tile_expert, uint32_t *__restrict__ tile_row0,
     uint32_t *__restrict__ tile_count) {
-  extern __shared__ uint32_t sh[];
-  uint32_t *cnt = sh;              // E + 1
-  uint32_t *tbase = sh + E + 1;    // E + 1
-  uint32_t *offs = sh + 2 * (E + 1); // E + 1
-  for (int e = threadIdx.x; e <= E; e += kSortThreads) cnt[e] = 0;
-  __syncthreads();
-  for (int a = threadIdx.x; a < A; a += kSortThreads) {
-    const uint32_t id = ids[a];
-    atomicAdd(&cnt[id < (uint32_t)E ? id : (uint32_t)E], 1u);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t run = 0, tiles = 0;
-    for (int e = 0; e <= E; ++e) {
-      const uint32_t c = cnt[e];
-      offsets[e] = run;
-      offs[e] = run;
-      tbase[e] = tiles;
-      run += c;
-      if (e < E) tiles += (c + kGemmBM - 1) / kGemmBM;
+  __shared__ uint32_t wsum[2][kScanThreads / 64];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int nb = E + 1;
+  // thread e owns bucket e (E + 1 <= 1025 buckets: thread 0 also takes bucket 1024)
+  auto scan_bucket = [&](int e, uint32_t &total, uint32_t &tiles) {
+    total = 0;
+    tiles = 0;
+    if (e < nb) {
+      for (int c = 0; c < nchunks; ++c) total += hist[(size_t)c * nb + e];
+      if (e < E) tiles = (total + kGemmBM - 1) / kGemmBM;
     }
-    offsets[E + 1] = run;
-    *tile_count = tiles;
+  };
+  uint32_t total, tiles;
+  scan_bucket(threadIdx.x, total, tiles);
+  uint32_t extra_total = 0, extra_tiles = 0;
+  if (threadIdx.x == 0 && nb > kScanThreads) scan_bucket(kScanThreads, extra_total, extra_tiles);
+  // block exclusive scans of total and tiles
+  uint32_t it = total, ip = tiles;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)it, off, kWave);
+    const uint32_t q = (uint32_t)__shfl_up((int)ip, off, kWave);
+    if (lane >= off) {
+      it += o;
+      ip += q;
+    }
+  }
+  if (lane == 63) {
+    wsum[0][w] = it;
+    wsum[1][w] = ip;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += kSortThreads) {
-    const uint32_t c = cnt[e], nt = (c + kGemmBM - 1) / kGemmBM;
-    const uint32_t first = offs[e];
-    for (uint32_t i = 0; i < nt; ++i) {
-      tile_expert[tbase[e] + i] = (uint32_t)e;
-      tile_row0[tbase[e] + i] = first + i * kGemmBM;
+  uint32_t bt = 0, bp = 0;
+  for (int v = 0; v < w; ++v) {
+    bt += wsum[0][v];
+    bp += wsum[1][v];
+  }
+  const uint32_t off_e = bt + it - total, tile0 = bp + ip - tiles;
+  const int e = threadIdx.x;
+  if (e < nb) {
+    offsets[e] = off_e;
+    uint32_t run = off_e;
+    for (int c = 0; c < nchunks; ++c) {
+      const uint32_t h = hist[(size_t)c * nb + e];
+      hist[(size_t)c * nb + e] = run;
+      run += h;
+    }
+    for (uint32_t i = 0; i < tiles; ++i) {
+      tile_expert[tile0 + i] = (uint32_t)e;
+      tile_row0[tile0 + i] = off_e + i * kGemmBM;
+    }
+  }
+  if (threadIdx.x == 0 && nb > kScanThreads) {
+    // bucket 1024 (ids >= E when E = 1024): after every other bucket
+    uint32_t run = (uint32_t)A - extra_total;
+    offsets[kScanThreads] = run;
+    for (int c = 0; c < nchunks; ++c) {
+      const uint32_t h = hist[(size_t)c * nb + kScanThreads];
+      hist[(size_t)c * nb + kScanThreads] = run;
+      run += h;
+    }
+  }
+  if (threadIdx.x == kScanThreads - 1 || (int)threadIdx.x == nb - 1) {
+    // the last bucket's thread knows the totals
+    if ((int)threadIdx.x == min(nb, kScanThreads) - 1) {
+      offsets[nb] = (uint32_t)A;
+      *tile_count = bp + ip;
     }
   }
 }
 
-// One workgroup per bucket (expert, or the trailing out-of-range bucket).  Thread j
-// owns a contiguous segment of slots; a block-wide exclusive scan of the per-segment
-// match counts gives each match its rank, so ties keep ascending slot order (stable).
-constexpr int kScatterThreads = 256;
-__global__ __launch_bounds__(kScatterThreads) void sort_scatter_kernel(
-    const uint32_t *__restrict__ ids, int A, int E, const uint32_t *__restrict__ offsets,
-    uint32_t *__restrict__ sorted_order, uint32_t *__restrict__ inverse_order,
-    uint32_t *__restrict__ sorted_ids) {
-  __shared__ uint32_t wsum[kScatterThreads / 64];
-  const uint32_t bucket = blockIdx.x;
-  const uint32_t begin = offsets[bucket], count = offsets[bucket + 1] - begin;
-  if (count == 0) return;
-  const int seg = (A + kScatterThreads - 1) / kScatterThreads;
-  const int a0 = threadIdx.x * seg, a1 = min(A, a0 + seg);
-  auto bucket_of = [&](uint32_t id) { return id < (uint32_t)E ? id : (uint32_t)E; };
-  // count pass: 16 independent loads in flight per step
-  uint32_t mine = 0;
-  for (int base = a0; base < a1; base += 16) {
-    uint32_t v[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = base + j < a1 ? ids[base + j] : 0u;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) mine += (base + j < a1) && bucket_of(v[j]) == bucket;
-  }
-  // block exclusive scan of `mine`
-  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  uint32_t incl = mine;
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t o = (uint32_t)__shfl_up((int)incl, off, kWave);
-    if (lane >= off) incl += o;
-  }
-  if (lane == 63) wsum[w] = incl;
-  __syncthreads();
-  uint32_t before = 0;
-  for (int i = 0; i < w; ++i) before += wsum[i];
-  uint32_t pos = begin + before + incl - mine;
-  for (int base = a0; base < a1 && mine; base += 16) {
-    uint32_t v[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = base + j < a1 ? ids[base + j] : 0u;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int a = base + j;
-      if (a < a1 && bucket_of(v[j]) == bucket) {
-        sorted_order[pos] = (uint32_t)a;
-        sorted_ids[pos] = v[j];
-        inverse_order[a] = pos;
-        ++pos;
-        --mine;
-      }
-    }
-  }
+// scatter: pos = base of (chunk, bucket) + chunk-local rank
+__global__ __launch_bounds__(kChunk) void sort_scatter_kernel(
+    const uint32_t *__restrict__ ids, int A, int E, const uint32_t *__restrict__ base,
+    const uint32_t *__restrict__ local_rank, uint32_t *__restrict__ sorted_order,
+    uint32_t *__restrict__ inverse_order, uint32_t *__restrict__ sorted_ids) {
+  const int a = blockIdx.x * kChunk + threadIdx.x;
+  if (a >= A) return;
+  const uint32_t id = ids[a];
+  const uint32_t b = id < (uint32_t)E ? id : (uint32_t)E;
+  const uint32_t pos = base[(size_t)blockIdx.x * (E + 1) + b] + local_rank[a];
+  sorted_order[pos] = (uint32_t)a;
+  sorted_ids[pos] = id;
+  inverse_order[a] = pos;
 }
 
 }  // namespace
@@ -154,17 +191,30 @@ hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int no
 
 int sort_max_tiles(int A, int E) { return A / kGemmBM + E + 1; }
 
+size_t sort_scratch_bytes(int A, int E) {
+  const size_t nchunks = ((size_t)A + kChunk - 1) / kChunk;
+  return ((nchunks * ((size_t)E + 1) * 4 + 255) & ~(size_t)255) + (size_t)A * 4;
+}
+
 hipError_t launch_sort(const uint32_t *ids, int A, int E, uint32_t *sorted_order,
                        uint32_t *inverse_order, uint32_t *sorted_ids, uint32_t *offsets,
                        uint32_t *tile_expert, uint32_t *tile_row0, uint32_t *tile_count,
-                       hipStream_t s) {
-  const size_t sh = sizeof(uint32_t) * 3 * ((size_t)E + 1);
-  hipLaunchKernelGGL(sort_count_kernel, dim3(1), dim3(kSortThreads), sh, s, ids, A, E, offsets,
+                       uint32_t *scratch, hipStream_t s) {
+  const int nchunks = (A + kChunk - 1) / kChunk;
+  uint32_t *hist = scratch;
+  uint32_t *local_rank = (uint32_t *)((char *)scratch + (((size_t)nchunks * (E + 1) * 4 + 255) & ~(size_t)255));
+  if (nchunks > 0) {
+    hipLaunchKernelGGL(sort_rank_kernel, dim3(nchunks), dim3(kChunk), sizeof(uint16_t) * 16 * ((size_t)E + 1),
+                       s, ids, A, E, hist, local_rank);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, hist, nchunks, A, E, offsets,
                      tile_expert, tile_row0, tile_count);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || A == 0) return err;
-  hipLaunchKernelGGL(sort_scatter_kernel, dim3(E + 1), dim3(kScatterThreads), 0, s, ids, A, E,
-                     offsets, sorted_order, inverse_order, sorted_ids);
+  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nchunks), dim3(kChunk), 0, s, ids, A, E, hist, local_rank,
+                     sorted_order, inverse_order, sorted_ids);
   return hipGetLastError();
 }
 
