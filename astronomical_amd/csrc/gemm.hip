@@ -604,6 +604,109 @@ hipError_t launch_ws(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_t 
   return launch(ws_gemm_kernel<kEpiPlain>, 2);
 }
 
+// Dense bf16 weights over one implicit group of rows (the router projection at prefill
+// sizes, N = experts is small): a 32-row x 64-column output tile per 4-wave workgroup, so
+// that even N = 256 gives M / 32 * 4 workgroups.  Operands go straight from global memory
+// into MFMA registers: wave w owns columns 16 w .. +16 of the tile and both 16-row blocks,
+// lane (c, q) loading 8 consecutive inputs q * 8 .. +8 of each 32-input step of its row /
+// weight row.  The four waves read the same activation rows (the vector L1 serves the
+// repeats).  K advances 256 at a time; the loads of the next 256 are issued before the
+// MFMAs of the current ones.  Workgroups of one 32-row block share an XCD.
+constexpr int DT_M = 32, DT_N = 64, DT_K = 256, DT_J = DT_K / 32;
+
+struct DenseFrag {
+  u32x4 a0[DT_J], a1[DT_J], b[DT_J];
+};
+
+__device__ __forceinline__ void dense_load(DenseFrag &f, const uint16_t *a0, const uint16_t *a1,
+                                           const uint16_t *bp, int k0) {
+#pragma unroll
+  for (int j = 0; j < DT_J; ++j) {
+    f.a0[j] = *(const u32x4 *)(a0 + k0 + 32 * j);
+    f.a1[j] = *(const u32x4 *)(a1 + k0 + 32 * j);
+    f.b[j] = *(const u32x4 *)(bp + k0 + 32 * j);
+  }
+}
+
+__device__ __forceinline__ void dense_mfma(const DenseFrag &f, f32x4 &acc0, f32x4 &acc1) {
+#pragma unroll
+  for (int j = 0; j < DT_J; ++j) {
+    const bf16x8 b = __builtin_bit_cast(bf16x8, f.b[j]);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.a0[j]), b, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.a1[j]), b, acc1, 0, 0, 0);
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void dense_gemm_kernel(const GemmArgs p, int nrb, int ncb) {
+  const int blk = blockIdx.x;
+  const int rb = (blk & 7) + 8 * (blk / (8 * ncb));
+  const int cb = (blk >> 3) % ncb;
+  if (rb >= nrb) return;  // grid padding to whole rounds of 8 row blocks
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, kq = lane >> 4;
+  const int r0 = rb * DT_M + c16, r1 = r0 + 16;
+  const int n = cb * DT_N + wave * 16 + c16;
+  const uint16_t *a0 = p.A + (int64_t)(r0 < p.M ? r0 : p.M - 1) * p.lda + kq * 8;
+  const uint16_t *a1 = p.A + (int64_t)(r1 < p.M ? r1 : p.M - 1) * p.lda + kq * 8;
+  const uint16_t *bp = p.bd + (int64_t)(n < p.N ? n : p.N - 1) * p.bd_row_stride + kq * 8;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  const int kmain = p.K / DT_K * DT_K;
+  if (kmain > 0) {
+    DenseFrag f0, f1;
+    dense_load(f0, a0, a1, bp, 0);
+    // ping-pong over two register sets; the last prefetch re-reads the final chunk
+    for (int k0 = 0; k0 < kmain; k0 += 2 * DT_K) {
+      const int k1 = k0 + DT_K < kmain ? k0 + DT_K : kmain - DT_K;
+      dense_load(f1, a0, a1, bp, k1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+      dense_mfma(f0, acc0, acc1);
+      if (k0 + DT_K >= kmain) break;
+      const int k2 = k0 + 2 * DT_K < kmain ? k0 + 2 * DT_K : kmain - DT_K;
+      dense_load(f0, a0, a1, bp, k2);
+      __builtin_amdgcn_sched_barrier(0);
+      dense_mfma(f1, acc0, acc1);
+    }
+  }
+  for (int k0 = kmain; k0 < p.K; k0 += 32) {  // K % 256 tail, 32 at a time
+    const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4 *)(bp + k0));
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4 *)(a0 + k0)), b, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4 *)(a1 + k0)), b, acc1, 0, 0, 0);
+  }
+  // lane holds column c16 of rows 4 kq + i of each 16-row block
+  if (n >= p.N) return;
+  const float bias = EPI == kEpiBias ? bf2f(p.bias[n]) : 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb * DT_M + h * 16 + kq * 4 + i;
+      if (r >= p.M) continue;
+      float v = h ? acc1[i] : acc0[i];
+      if (EPI == kEpiBias) v = round_bf(v) + bias;
+      p.C[(int64_t)r * p.ldc + n] = (uint16_t)f2bf(v);
+    }
+  }
+}
+
+hipError_t launch_dense(const GemmArgs &a, int epi, hipStream_t s) {
+  const int nrb = (a.M + DT_M - 1) / DT_M, ncb = (a.N + DT_N - 1) / DT_N;
+  const int grid = ((nrb + 7) & ~7) * ncb;
+  if (epi == kEpiBias)
+    hipLaunchKernelGGL(dense_gemm_kernel<kEpiBias>, dim3(grid), dim3(256), 0, s, a, nrb, ncb);
+  else
+    hipLaunchKernelGGL(dense_gemm_kernel<kEpiPlain>, dim3(grid), dim3(256), 0, s, a, nrb, ncb);
+  return hipGetLastError();
+}
+
+bool use_dense(const GemmArgs &a, int epi) {
+  // one implicit group, bf16 weights, 16-B aligned 32-input steps, no row indirection
+  return a.bkind == kBDense && !a.tile_expert && !a.a_rows && !a.c_rows && epi != kEpiSwiglu &&
+         a.K % 32 == 0 && a.lda % 8 == 0 && a.bd_row_stride % 8 == 0 && a.M > 0 && a.N > 0 &&
+         ((uintptr_t)a.A & 15) == 0 && ((uintptr_t)a.bd & 15) == 0;
+}
+
 bool use_ws(const GemmArgs &a) {
   // 4-bit weights with K steps of 64 and an even number of groups of >= 32 inputs per row
   // (one dword of scales per step stays 4-byte aligned); K >= 1024: with fewer K steps its
@@ -626,6 +729,7 @@ hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilog
     const hipError_t e = launch_grouped_gemm2(a, nullptr, epilogue, s);
     return e == hipSuccess ? launch_grouped_gemm2(*b, nullptr, epilogue, s) : e;
   }
+  if (!b && use_dense(a, epilogue)) return launch_dense(a, epilogue, s);
   if (use_ws(a)) return launch_ws(a, b, epilogue, s);
   switch (a.bkind) {
     case kBQ4: return launch_kind<kBQ4>(a, b, epilogue, s);
