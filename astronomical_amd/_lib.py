@@ -44,11 +44,22 @@ class WorkspaceView(C.Structure):
     _fields_ = [("total_bytes", C.c_size_t), ("sorted_path", C.c_int32)] + [
         (n, C.c_size_t) for n in ("logits", "indices", "scores", "sorted_order", "inverse_order",
                                   "sorted_ids", "expert_offsets", "activated", "activated_ld", "expert_out",
-                                  "sparse", "shared_out", "shared_gate_logits")]
+                                  "sparse", "shared_out", "shared_gate_logits", "expert_slots",
+                                  "missing_slots")]
 
 
 EXPORTS = {
     # name: (argtypes, restype)
+    "astro_moe_remap_expert_slots": ([C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p,
+                                      C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_gather_assignments": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
+                                      C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_streamed_sparse_workspace_bytes": ([C.POINTER(Layer), C.c_int32, C.c_int32,
+                                                   C.POINTER(C.c_size_t)], C.c_int),
+    "astro_moe_streamed_sparse_forward": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p,
+                                           C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                                           C.c_size_t, C.c_void_p], C.c_int),
+    "astro_moe_add": ([C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
     "astro_moe_last_error": ([], C.c_char_p),
     "astro_moe_abi_version": ([], C.c_int),
     "astro_moe_workspace_bytes": ([C.POINTER(Layer), C.c_int32, C.POINTER(C.c_size_t)], C.c_int),

@@ -107,7 +107,8 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Layout {
   size_t logits, idx, scores, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
-      tile_count, act, eout, sparse, shared_act, shared_out, z, groups, sort_scratch, total;
+      tile_count, act, eout, sparse, shared_act, shared_out, z, groups, sort_scratch, slots, missing,
+      total;
   int max_tiles;
   bool decode;     // wavefront-GEMV path: act / eout hold A routed rows then T shared rows
   int64_t act_ld;  // row length of act
@@ -115,21 +116,31 @@ struct Layout {
 
 // The decode path takes small batches: at most 8 tokens and 64 assignments, a dense router,
 // and shapes its per-lane register tiles cover (decode.hip: decode_supported).
+// Leading dimension of the routed expert arrays: the expert count for resident weights, the
+// page's slot count for compact pages (slot_of_expert set).
+int expert_capacity(const astro_moe_layer &L) {
+  return L.gate_up.w ? L.gate_up.experts : L.gate.experts;
+}
+
 bool decode_path(const astro_moe_layer &L, int T) {
   const int Is = L.shared_intermediate > 0 ? L.shared_intermediate : 0;
   const astro_moe_affine &gu = L.gate_up.w ? L.gate_up : L.gate;
-  return T >= 1 && T <= 8 && T * L.top_k <= 64 && L.top_k <= kDecodeMaxK &&
+  return !L.slot_of_expert && T >= 1 && T <= 8 && T * L.top_k <= 64 && L.top_k <= kDecodeMaxK &&
          L.router_w != nullptr && L.hidden <= 4096 &&
          L.intermediate <= 1024 && Is <= 1024 && (gu.bits == 4 || gu.bits == 8) &&
          (L.down.bits == 4 || L.down.bits == 8) &&
          (Is == 0 || L.shared_down.bits == L.down.bits);
 }
 
-Layout block_layout(const astro_moe_layer &L, int T) {
+// Workspace of the block (kk = top_k) or of the streamed sparse forward (kk = assignments per
+// token, no routing and no shared expert: with_router = false).
+Layout block_layout(const astro_moe_layer &L, int T, int kk, bool with_router) {
   Layout o{};
-  const size_t A = (size_t)T * L.top_k, E = (size_t)L.num_experts;
-  const size_t Is = L.shared_intermediate > 0 ? (size_t)L.shared_intermediate : 0;
-  o.decode = decode_path(L, T);
+  const size_t A = (size_t)T * kk;
+  // ids the sort buckets: expert ids, or page slots
+  const size_t E = (size_t)std::max(L.num_experts, expert_capacity(L));
+  const size_t Is = with_router && L.shared_intermediate > 0 ? (size_t)L.shared_intermediate : 0;
+  o.decode = with_router && decode_path(L, T);
   o.max_tiles = o.decode ? 0 : sort_max_tiles((int)A, (int)E);
   size_t p = 0;
   auto take = [&](size_t bytes) {
@@ -137,7 +148,7 @@ Layout block_layout(const astro_moe_layer &L, int T) {
     p = align_up(p + bytes);
     return at;
   };
-  o.logits = take((size_t)T * E * 2);
+  o.logits = take(with_router ? (size_t)T * L.num_experts * 2 : 0);
   o.idx = take(A * 4);
   o.scores = take(A * 2);
   o.sorted_order = take(A * 4);
@@ -165,9 +176,39 @@ Layout block_layout(const astro_moe_layer &L, int T) {
     o.shared_act = take((size_t)T * Is * 2);
     o.shared_out = take(Is ? (size_t)T * L.hidden * 2 : 0);
     o.z = take(Is ? (size_t)T * 2 : 0);
+    o.slots = take(with_router && L.slot_of_expert ? A * 4 : 0);
+    o.missing = take(with_router && L.slot_of_expert ? 4 : 0);
   }
   o.total = p;
   return o;
+}
+
+// The routed expert arrays: fused gate/up or separate gate and up, and down, all with
+// `capacity` experts (the expert count, or a compact page's slots).
+int check_routed(const char *op, const astro_moe_layer *L, int capacity) {
+  const int H = L->hidden, I = L->intermediate;
+  if (capacity <= 0 || capacity > 1024)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "expert arrays must hold between 1 and 1024 experts or page slots");
+  if (H % 64 != 0 || I % 64 != 0)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "the gfx950 kernels need hidden and intermediate sizes that are multiples of 64");
+  if (L->gate_up.w) {
+    int rc = check_affine(op, &L->gate_up, H);
+    if (rc) return rc;
+    if (L->gate_up.experts != capacity || L->gate_up.out_features != 2 * I)
+      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "resident fused gate/up output dimension must be twice the intermediate size");
+  } else {
+    int rc = check_affine(op, &L->gate, H);
+    if (!rc) rc = check_affine(op, &L->up, H);
+    if (rc) return rc;
+    if (L->gate.experts != capacity || L->up.experts != capacity || L->gate.out_features != I ||
+        L->up.out_features != I || L->gate.bits != L->up.bits || L->gate.group_size != L->up.group_size)
+      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "separate gate and up projections must share shape and quantization");
+  }
+  int rc = check_affine(op, &L->down, I);
+  if (rc) return rc;
+  if (L->down.experts != capacity || L->down.out_features != H)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "down projection must map the intermediate size back to the hidden size");
+  return ASTRO_MOE_OK;
 }
 
 int check_layer(const char *op, const astro_moe_layer *L) {
@@ -180,8 +221,6 @@ int check_layer(const char *op, const astro_moe_layer *L) {
                 "selected expert count must be positive and no larger than the router dimension");
   if (E > 1024 || k > 64)
     return fail(ASTRO_MOE_UNSUPPORTED, op, "the router kernel supports at most 1024 experts and top-64");
-  if (L->slot_of_expert)
-    return fail(ASTRO_MOE_UNSUPPORTED, op, "compact page slots are not implemented in this version");
   if (!!L->router_w == !!L->router_q.w)
     return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "exactly one of the dense and affine router weights must be set");
   if (L->router_q.w) {
@@ -190,26 +229,11 @@ int check_layer(const char *op, const astro_moe_layer *L) {
     if (L->router_q.experts != 1 || L->router_q.out_features != E)
       return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "router weights must map the hidden size to the expert count");
   }
-  if (H % 64 != 0 || I % 64 != 0)
-    return fail(ASTRO_MOE_UNSUPPORTED, op, "the gfx950 kernels need hidden and intermediate sizes that are multiples of 64");
-  if (L->gate_up.w) {
-    int rc = check_affine(op, &L->gate_up, H);
-    if (rc) return rc;
-    if (L->gate_up.experts != E || L->gate_up.out_features != 2 * I)
-      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "resident fused gate/up output dimension must be twice the intermediate size");
-  } else {
-    int rc = check_affine(op, &L->gate, H);
-    if (!rc) rc = check_affine(op, &L->up, H);
-    if (rc) return rc;
-    if (L->gate.experts != E || L->up.experts != E || L->gate.out_features != I ||
-        L->up.out_features != I || L->gate.bits != L->up.bits || L->gate.group_size != L->up.group_size)
-      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "separate gate and up projections must share shape and quantization");
-  }
   {
-    int rc = check_affine(op, &L->down, I);
+    // resident arrays hold every expert; a compact page (slot_of_expert set) any slot count
+    const astro_moe_affine &first = L->gate_up.w ? L->gate_up : L->gate;
+    int rc = check_routed(op, L, L->slot_of_expert ? first.experts : E);
     if (rc) return rc;
-    if (L->down.experts != E || L->down.out_features != H)
-      return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "down projection must map the intermediate size back to the hidden size");
   }
   if (L->shared_intermediate < 0)
     return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "shared expert intermediate size must not be negative");
@@ -312,6 +336,101 @@ struct StageClock {
   void end(int i) { (void)hipEventRecord(ev[2 * i + 1], s); }
 };
 
+// The sparse graph after routing (forward_moe_with_streamed_weights, paged_execution.rs:207-281,
+// and the resident arm of resident_execution.rs:70-143): sort the assignments by id (expert or
+// page slot), gate/up with the SwiGLU epilogue over rows x[sorted_order[r] / kk], down, and the
+// weighted sum -- sorted rounding iff A >= 64 (routing.rs:13).  with_shared: the shared
+// expert's gate/up and down run in the routed launches and y = the shared combine; otherwise
+// y = the sparse output.
+hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk, const uint32_t *ids,
+                      const uint16_t *scores, const Layout &o, char *ws, bool with_shared, uint16_t *y,
+                      hipStream_t s, StageClock *clock) {
+  auto at = [&](size_t off) { return (void *)(ws + off); };
+  auto begin = [&](int i) {
+    if (clock) clock->begin(i);
+  };
+  auto end = [&](int i) {
+    if (clock) clock->end(i);
+  };
+  const int H = L.hidden, I = L.intermediate, A = T * kk;
+  const int E = std::max(L.num_experts, expert_capacity(L));
+  uint32_t *sorted_order = (uint32_t *)at(o.sorted_order);
+  uint32_t *inverse = (uint32_t *)at(o.inverse);
+  uint32_t *sorted_ids = (uint32_t *)at(o.sorted_ids);
+  uint32_t *offsets = (uint32_t *)at(o.offsets);
+  uint32_t *tile_expert = (uint32_t *)at(o.tile_expert);
+  uint32_t *tile_row0 = (uint32_t *)at(o.tile_row0);
+  uint32_t *tile_count = (uint32_t *)at(o.tile_count);
+  uint16_t *act = (uint16_t *)at(o.act);
+  uint16_t *eout = (uint16_t *)at(o.eout);
+  uint16_t *sparse = (uint16_t *)at(o.sparse);
+  const bool has_shared = with_shared && L.shared_intermediate > 0;
+  uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
+  uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
+
+  begin(2);
+  hipError_t e = launch_sort(ids, A, E, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
+                             tile_count, (uint32_t *)at(o.sort_scratch), s);
+  end(2);
+  if (e != hipSuccess) return e;
+
+  // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / kk]
+  GemmArgs gu{};
+  gu.A = x;
+  gu.lda = H;
+  gu.a_rows = sorted_order;
+  gu.a_div = kk;
+  gu.K = H;
+  gu.N = I;
+  if (L.gate_up.w)
+    set_weights(gu, L.gate_up, &L.gate_up, I);
+  else
+    set_weights(gu, L.gate, &L.up, 0);
+  gu.tile_expert = tile_expert;
+  gu.tile_row0 = tile_row0;
+  gu.tile_count = tile_count;
+  gu.expert_offsets = offsets;
+  gu.max_tiles = o.max_tiles;
+  gu.C = act;
+  gu.ldc = I;
+  // the shared expert's gate/up and down run in the same launches as the routed ones
+  GemmArgs sgu, sdn;
+  if (has_shared)
+    shared_gemm_args(L, x, T, (uint16_t *)at(o.shared_act), shared_out, sgu, sdn);
+  begin(3);
+  e = launch_grouped_gemm2(gu, has_shared ? &sgu : nullptr, kEpiSwiglu, s);
+  end(3);
+
+  GemmArgs dn{};
+  dn.A = act;
+  dn.lda = I;
+  dn.a_div = 1;
+  dn.K = I;
+  dn.N = H;
+  set_weights(dn, L.down, nullptr, 0);
+  dn.tile_expert = tile_expert;
+  dn.tile_row0 = tile_row0;
+  dn.tile_count = tile_count;
+  dn.expert_offsets = offsets;
+  dn.max_tiles = o.max_tiles;
+  dn.C = eout;
+  dn.ldc = H;
+  begin(4);
+  if (e == hipSuccess) e = launch_grouped_gemm2(dn, has_shared ? &sdn : nullptr, kEpiPlain, s);
+  end(4);
+
+  if (has_shared) {
+    begin(5);
+    if (e == hipSuccess) e = run_shared_gate(L, x, T, z, s);
+    end(5);
+  }
+  begin(6);
+  if (e == hipSuccess)
+    e = launch_combine(eout, inverse, scores, T, kk, H, A >= 64, shared_out, z, sparse, y, s);
+  end(6);
+  return e;
+}
+
 // The block's launch sequence; clock (nullable) collects per-stage times.
 int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, uint16_t *y,
               void *workspace, size_t workspace_bytes, void *stream, StageClock *clock) {
@@ -321,7 +440,7 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   if (tokens == 0) return ok();
   if (!x || !y) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "hidden states and output must be non-null");
   const astro_moe_layer &L = *layer;
-  const Layout o = block_layout(L, tokens);
+  const Layout o = block_layout(L, tokens, L.top_k, true);
   if (!workspace || workspace_bytes < o.total) return workspace_fail(kBlockOp, o.total, workspace ? workspace_bytes : 0);
   hipStream_t s = (hipStream_t)stream;
   char *ws = (char *)workspace;
@@ -456,69 +575,18 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   end(0);
   begin(1);
   if (e == hipSuccess) e = launch_route_topk(logits, T, E, k, L.normalize_top_k, idx, scores, s);
-  end(1);
-  begin(2);
-  if (e == hipSuccess)
-    e = launch_sort(idx, A, E, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
-                    tile_count, (uint32_t *)at(o.sort_scratch), s);
-  end(2);
-  if (e != hipSuccess) return hip_fail(kBlockOp, e);
-
-  // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / k]
-  GemmArgs gu{};
-  gu.A = x;
-  gu.lda = H;
-  gu.a_rows = sorted_order;
-  gu.a_div = k;
-  gu.K = H;
-  gu.N = I;
-  if (L.gate_up.w)
-    set_weights(gu, L.gate_up, &L.gate_up, I);
-  else
-    set_weights(gu, L.gate, &L.up, 0);
-  gu.tile_expert = tile_expert;
-  gu.tile_row0 = tile_row0;
-  gu.tile_count = tile_count;
-  gu.expert_offsets = offsets;
-  gu.max_tiles = o.max_tiles;
-  gu.C = act;
-  gu.ldc = I;
-  // the shared expert's gate/up and down run in the same launches as the routed ones
-  GemmArgs sgu, sdn;
-  if (has_shared)
-    shared_gemm_args(L, x, T, (uint16_t *)at(o.shared_act), shared_out, sgu, sdn);
-  begin(3);
-  e = launch_grouped_gemm2(gu, has_shared ? &sgu : nullptr, kEpiSwiglu, s);
-  end(3);
-
-  GemmArgs dn{};
-  dn.A = act;
-  dn.lda = I;
-  dn.a_div = 1;
-  dn.K = I;
-  dn.N = H;
-  set_weights(dn, L.down, nullptr, 0);
-  dn.tile_expert = tile_expert;
-  dn.tile_row0 = tile_row0;
-  dn.tile_count = tile_count;
-  dn.expert_offsets = offsets;
-  dn.max_tiles = o.max_tiles;
-  dn.C = eout;
-  dn.ldc = H;
-  begin(4);
-  if (e == hipSuccess) e = launch_grouped_gemm2(dn, has_shared ? &sdn : nullptr, kEpiPlain, s);
-  end(4);
-
-  if (has_shared) {
-    begin(5);
-    if (e == hipSuccess) e = run_shared_gate(L, x, T, z, s);
-    end(5);
+  // compact pages (forward_moe_paged, paged_execution.rs:98-139): the expert ids become page
+  // slots (qwen3_5_moe_remap_expert_page_slots, split_page_route.rs:79-105) before the sort
+  const uint32_t *ids = idx;
+  if (e == hipSuccess && L.slot_of_expert) {
+    uint32_t *slots = (uint32_t *)at(o.slots), *missing = (uint32_t *)at(o.missing);
+    e = launch_zero_u32(missing, 1, s);
+    if (e == hipSuccess) e = launch_remap_slots(idx, A, L.slot_of_expert, E, slots, missing, s);
+    ids = slots;
   }
-  // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
-  begin(6);
-  if (e == hipSuccess)
-    e = launch_combine(eout, inverse, scores, T, k, H, A >= 64, shared_out, z, sparse, y, s);
-  end(6);
+  end(1);
+  if (e != hipSuccess) return hip_fail(kBlockOp, e);
+  e = run_sparse(L, x, T, k, ids, scores, o, ws, true, y, s, clock);
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
   return ok();
 }
@@ -535,7 +603,7 @@ int astro_moe_workspace_bytes(const astro_moe_layer *layer, int32_t tokens, size
   int rc = check_layer(kBlockOp, layer);
   if (rc) return rc;
   if (tokens < 0 || !bytes) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
-  *bytes = block_layout(*layer, tokens).total;
+  *bytes = block_layout(*layer, tokens, layer->top_k, true).total;
   return ok();
 }
 
@@ -544,7 +612,7 @@ int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
   int rc = check_layer(kBlockOp, layer);
   if (rc) return rc;
   if (tokens < 0 || !view) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
-  const Layout o = block_layout(*layer, tokens);
+  const Layout o = block_layout(*layer, tokens, layer->top_k, true);
   view->total_bytes = o.total;
   view->sorted_path = (int64_t)tokens * layer->top_k >= 64;
   view->logits = o.logits;
@@ -560,6 +628,8 @@ int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
   view->sparse = o.sparse;
   view->shared_out = o.shared_out;
   view->shared_gate_logits = o.z;
+  view->expert_slots = o.slots;
+  view->missing_slots = o.missing;
   return ok();
 }
 
@@ -827,6 +897,76 @@ int astro_moe_shared_expert(const astro_moe_layer *layer, const uint16_t *x, int
   hipError_t e = run_shared(*layer, x, tokens, (uint16_t *)workspace, shared_out, gate_logits,
                             (hipStream_t)stream);
   return e == hipSuccess ? ok() : hip_fail(kCombineOp, e);
+}
+
+
+int astro_moe_remap_expert_slots(const uint32_t *expert_ids, int32_t n, const uint32_t *slot_of_expert,
+                                 int32_t experts, uint32_t *slots, uint32_t *missing_count, void *stream) {
+  const char *op = "remap Qwen3.5-MoE expert page slots";
+  if (n < 0 || experts <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "assignment count must not be negative and the expert capacity positive");
+  if (n == 0) return ok();
+  if (!expert_ids || !slot_of_expert || !slots)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "expert ids, the slot map and the slot output must be non-null");
+  hipError_t e = launch_remap_slots(expert_ids, n, slot_of_expert, experts, slots, missing_count, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(op, e);
+}
+
+int astro_moe_gather_assignments(const uint32_t *ids, const uint16_t *scores, const uint32_t *positions,
+                                 int32_t n, uint32_t *out_ids, uint16_t *out_scores, void *stream) {
+  const char *op = "build Qwen3.5-MoE split expert page route";
+  if (n < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "assignment count must not be negative");
+  if (n == 0) return ok();
+  if (!positions || (out_ids && !ids) || (out_scores && !scores))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "positions and the source of every requested output must be non-null");
+  hipError_t e = launch_gather_assignments(ids, scores, positions, n, out_ids, out_scores, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(op, e);
+}
+
+static int check_page(const char *op, const astro_moe_layer *page) {
+  if (!page) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "page description must be non-null");
+  if (page->hidden <= 0 || page->intermediate <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "hidden and intermediate sizes must be positive");
+  return check_routed(op, page, expert_capacity(*page));
+}
+
+static const char *const kStreamedOp = "run Qwen3.5-MoE experts from a streamed page";
+
+int astro_moe_streamed_sparse_workspace_bytes(const astro_moe_layer *page, int32_t tokens, int32_t per_token,
+                                              size_t *bytes) {
+  int rc = check_page(kStreamedOp, page);
+  if (rc) return rc;
+  if (tokens < 0 || per_token <= 0 || !bytes)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kStreamedOp, "token count must not be negative and assignments per token positive");
+  *bytes = block_layout(*page, tokens, per_token, false).total;
+  return ok();
+}
+
+int astro_moe_streamed_sparse_forward(const astro_moe_layer *page, const uint16_t *x, int32_t tokens,
+                                      const uint32_t *slots, const uint16_t *scores, int32_t per_token,
+                                      uint16_t *sparse, void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = check_page(kStreamedOp, page);
+  if (rc) return rc;
+  if (tokens < 0 || per_token <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kStreamedOp, "token count must not be negative and assignments per token positive");
+  if (tokens == 0) return ok();
+  if (!x || !slots || !scores || !sparse)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, kStreamedOp, "hidden states, slots, scores and output must be non-null");
+  const Layout o = block_layout(*page, tokens, per_token, false);
+  if (!workspace || workspace_bytes < o.total)
+    return workspace_fail(kStreamedOp, o.total, workspace ? workspace_bytes : 0);
+  hipError_t e = run_sparse(*page, x, tokens, per_token, slots, scores, o, (char *)workspace, false, sparse,
+                            (hipStream_t)stream, nullptr);
+  return e == hipSuccess ? ok() : hip_fail(kStreamedOp, e);
+}
+
+int astro_moe_add(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, void *stream) {
+  const char *op = "add";
+  if (n < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "element count must not be negative");
+  if (n == 0) return ok();
+  if (!a || !b || !out) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "operands and output must be non-null");
+  hipError_t e = launch_add_bf16(a, b, n, out, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(op, e);
 }
 
 }  // extern "C"

@@ -1,6 +1,7 @@
 // Bandwidth-bound pieces of the block: SwiGLU, the weighted expert combine with the
-// shared expert's gated add, and a skinny quantized GEMV (the shared expert's
-// 2048 -> 1 output gate).
+// shared expert's gated add, a skinny quantized GEMV (the shared expert's 2048 -> 1 output
+// gate), and the small index / add operations of the paged callers (page slot remap,
+// assignment gather, bf16 add).
 #include "common.h"
 #include "kernels.h"
 
@@ -199,7 +200,80 @@ void launch_combine_s(const uint16_t *rows, const uint32_t *inverse_order, const
     launch_combine_t<SORTED, 0>(rows, inverse_order, scores, T, k, D, shared_out, gate_logits, sparse_out, y, s);
 }
 
+// page slot of every assignment: slots[a] = slot_of_expert[ids[a]]; an id past the map or
+// a slot marked absent (0xffffffff) counts into *missing and reads slot 0 instead, so every
+// later weight access stays inside the page
+__global__ __launch_bounds__(256) void remap_slots_kernel(const uint32_t *__restrict__ ids, int n,
+                                                          const uint32_t *__restrict__ slot_of_expert,
+                                                          int experts, uint32_t *__restrict__ slots,
+                                                          uint32_t *__restrict__ missing) {
+  const int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a >= n) return;
+  const uint32_t e = ids[a];
+  uint32_t s = e < (uint32_t)experts ? slot_of_expert[e] : 0xffffffffu;
+  if (s == 0xffffffffu) {
+    if (missing) atomicAdd(missing, 1u);
+    s = 0;
+  }
+  slots[a] = s;
+}
+
+// out_ids[i] = ids[positions[i]], out_scores[i] = scores[positions[i]]
+__global__ __launch_bounds__(256) void gather_assignments_kernel(
+    const uint32_t *__restrict__ ids, const uint16_t *__restrict__ scores,
+    const uint32_t *__restrict__ positions, int n, uint32_t *__restrict__ out_ids,
+    uint16_t *__restrict__ out_scores) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t a = positions[i];
+  if (out_ids) out_ids[i] = ids[a];
+  if (out_scores) out_scores[i] = scores[a];
+}
+
+// a few words set to zero (a kernel, so that callers may capture it in a graph)
+__global__ __launch_bounds__(64) void zero_u32_kernel(uint32_t *__restrict__ p, int n) {
+  for (int i = threadIdx.x; i < n; i += 64) p[i] = 0;
+}
+
+// bf16 + bf16 -> bf16: the fp32 sum rounded to nearest even (MLX add on bf16 arrays)
+__global__ __launch_bounds__(256) void add_bf16_kernel(const uint16_t *__restrict__ a,
+                                                       const uint16_t *__restrict__ b, int64_t n,
+                                                       uint16_t *__restrict__ out) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = (uint16_t)f2bf(bf2f(a[i]) + bf2f(b[i]));
+}
+
 }  // namespace
+
+hipError_t launch_remap_slots(const uint32_t *ids, int n, const uint32_t *slot_of_expert, int experts,
+                              uint32_t *slots, uint32_t *missing, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(remap_slots_kernel, dim3((n + 255) / 256), dim3(256), 0, s, ids, n, slot_of_expert,
+                     experts, slots, missing);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_assignments(const uint32_t *ids, const uint16_t *scores,
+                                     const uint32_t *positions, int n, uint32_t *out_ids,
+                                     uint16_t *out_scores, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_assignments_kernel, dim3((n + 255) / 256), dim3(256), 0, s, ids, scores,
+                     positions, n, out_ids, out_scores);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_u32(uint32_t *p, int n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, s, p, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_bf16(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(add_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, n, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *out,
                          hipStream_t s) {

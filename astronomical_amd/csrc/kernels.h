@@ -74,6 +74,16 @@ hipError_t launch_qgemv_rows(const uint16_t *x, int T, int K, const uint32_t *w,
 
 hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *out,
                          hipStream_t s);
+
+// paged callers: slots[a] = slot_of_expert[ids[a]] (absent experts count into *missing and
+// read slot 0); assignment gather by position; bf16 add
+hipError_t launch_remap_slots(const uint32_t *ids, int n, const uint32_t *slot_of_expert, int experts,
+                              uint32_t *slots, uint32_t *missing, hipStream_t s);
+hipError_t launch_gather_assignments(const uint32_t *ids, const uint16_t *scores,
+                                     const uint32_t *positions, int n, uint32_t *out_ids,
+                                     uint16_t *out_scores, hipStream_t s);
+hipError_t launch_add_bf16(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, hipStream_t s);
+hipError_t launch_zero_u32(uint32_t *p, int n, hipStream_t s);  // a kernel, safe in graph capture
 // y = weighted sum of expert rows (rows located through inverse_order), sorted (fp32
 // fma accumulation) or unsorted (bf16 products) rounding, then optionally the shared
 // expert's gated add.

@@ -139,6 +139,10 @@ class MoeLayerWeights:
     shared_down: Optional[AffineWeights] = None
     shared_expert_gate: Optional[AffineWeights] = None
     extras: dict = field(default_factory=dict)
+    # compact paged pages: u32 [E] global expert id -> slot of the routed arrays, 0xffffffff
+    # for experts the page does not hold (page_slot_by_global_expert_id,
+    # quantized_expert_manifest.rs:212-220); None for resident arrays
+    slot_of_expert: Optional[object] = None
 
     def map(self, fn) -> "MoeLayerWeights":
         def m(a):
@@ -148,7 +152,7 @@ class MoeLayerWeights:
             self.shared_intermediate, self.normalize_top_k, m(self.router_w), m(self.gate_up),
             m(self.down), m(self.gate), m(self.up), m(self.router_q), m(self.router_bias),
             m(self.shared_gate), m(self.shared_up), m(self.shared_down),
-            m(self.shared_expert_gate), dict(self.extras))
+            m(self.shared_expert_gate), dict(self.extras), m(self.slot_of_expert))
 
     def page_bytes(self) -> int:
         """Bytes of one routed expert's gate/up + down page (scales and biases included)."""

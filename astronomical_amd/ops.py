@@ -83,6 +83,7 @@ def layer_struct(L: MoeLayerWeights) -> Layer:
     s.shared_up = affine_struct(L.shared_up)
     s.shared_down = affine_struct(L.shared_down)
     s.shared_expert_gate = affine_struct(L.shared_expert_gate)
+    s.slot_of_expert = None if L.slot_of_expert is None else L.slot_of_expert.data_ptr()
     return s
 
 
@@ -342,6 +343,9 @@ class MoeBlock:
         L = self.weights
         T, E, k, H, I = tokens, L.num_experts, L.top_k, L.hidden, L.intermediate
         A = T * k
+        # the sort buckets page slots when the layer is a compact page
+        capacity = (L.gate_up if L.gate_up is not None else L.gate).experts
+        E_sort = max(E, capacity)
 
         def get(off, n, dt):
             return raw[off: off + n * np.dtype(dt).itemsize].view(dt).copy()
@@ -353,13 +357,16 @@ class MoeBlock:
             sorted_order=get(v.sorted_order, A, np.uint32),
             inverse_order=get(v.inverse_order, A, np.uint32),
             sorted_ids=get(v.sorted_ids, A, np.uint32),
-            expert_offsets=get(v.expert_offsets, E + 1, np.uint32),
+            expert_offsets=get(v.expert_offsets, E_sort + 1, np.uint32),
             activated_sorted=get(v.activated, A * v.activated_ld, np.uint16).reshape(A, v.activated_ld)[:, :I],
             expert_out_sorted=get(v.expert_out, A * H, np.uint16).reshape(A, H),
             sparse=get(v.sparse, T * H, np.uint16).reshape(T, H))
         if L.shared_intermediate:
             out["shared_out"] = get(v.shared_out, T * H, np.uint16).reshape(T, H)
             out["shared_gate_logits"] = get(v.shared_gate_logits, T, np.uint16)
+        if L.slot_of_expert is not None:
+            out["expert_slots"] = get(v.expert_slots, A, np.uint32).reshape(T, k)
+            out["missing_slots"] = int(get(v.missing_slots, 1, np.uint32)[0])
         return out
 
 
@@ -385,3 +392,122 @@ def shared_expert(weights: MoeLayerWeights, x: torch.Tensor):
     call("astro_moe_shared_expert", C.byref(s), _ptr(x2), T, _ptr(so), _ptr(z), _ptr(ws),
          need.value, _stream(x.device))
     return so, z
+
+
+# ------------------------------------------------------ paged callers (paged_execution.rs)
+
+SLOT_ABSENT = 0xFFFFFFFF
+_REMAP_OP = "remap Qwen3.5-MoE expert page slots"
+_SPLIT_OP = "build Qwen3.5-MoE split expert page route"
+
+
+def qwen3_5_moe_remap_expert_page_slots(selected_indices: torch.Tensor,
+                                        page_slot_by_global_expert_id: torch.Tensor) -> torch.Tensor:
+    """split_page_route.rs:79-105: page slot of every selected expert (int32, same shape).
+    Like the reference, refuses a routed expert the page does not hold; the check reads the
+    device's absent-expert count back (one stream synchronisation)."""
+    ids = selected_indices.contiguous().view(torch.int32)
+    m = page_slot_by_global_expert_id.contiguous().view(torch.int32)
+    slots = torch.empty_like(ids)
+    missing = torch.zeros(1, dtype=torch.int32, device=ids.device)
+    call("astro_moe_remap_expert_slots", _ptr(ids), ids.numel(), _ptr(m), m.numel(), _ptr(slots),
+         _ptr(missing), _stream(ids.device))
+    if int(missing.item()):
+        raise AstroMoeError(_lib.INVALID_ARGUMENT,
+                            f"{_REMAP_OP}: a routed expert is absent from the streamed page manifest")
+    return slots
+
+
+def forward_moe_with_streamed_weights(hidden_states: torch.Tensor, page: MoeLayerWeights,
+                                      page_slot_indices: torch.Tensor,
+                                      selected_scores: torch.Tensor) -> torch.Tensor:
+    """paged_execution.rs:207-281: the sparse expert output bf16 [T, H] of T tokens with
+    page_slot_indices / selected_scores [T, kk] against the page's routed arrays."""
+    s = layer_struct(page)
+    x2 = hidden_states.contiguous().view(torch.bfloat16).reshape(-1, page.hidden)
+    T = x2.shape[0]
+    slots = page_slot_indices.contiguous().view(torch.int32).reshape(T, -1)
+    sc = selected_scores.contiguous().view(torch.bfloat16).reshape(T, -1)
+    kk = slots.shape[1]
+    need = C.c_size_t()
+    call("astro_moe_streamed_sparse_workspace_bytes", C.byref(s), T, kk, C.byref(need))
+    ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x2.device)
+    out = torch.empty(T, page.hidden, dtype=torch.bfloat16, device=x2.device)
+    call("astro_moe_streamed_sparse_forward", C.byref(s), _ptr(x2), T, _ptr(slots), _ptr(sc), kk,
+         _ptr(out), _ptr(ws), need.value, _stream(x2.device))
+    return out
+
+
+def add(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """MlxRuntime::add of two bf16 arrays of one shape (fp32 sum, rounded to nearest even)."""
+    a2, b2 = a.contiguous().view(torch.bfloat16), b.contiguous().view(torch.bfloat16)
+    if a2.shape != b2.shape:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, "add: operands must have one shape")
+    out = torch.empty_like(a2)
+    call("astro_moe_add", _ptr(a2), _ptr(b2), a2.numel(), _ptr(out), _stream(a2.device))
+    return out
+
+
+@dataclass
+class Qwen3_5MoESplitPageRoute:
+    """split_page_route.rs:11-16."""
+    retained_page_slot_indices: torch.Tensor
+    retained_scores: torch.Tensor
+    missing_page_slot_indices: torch.Tensor
+    missing_scores: torch.Tensor
+
+    @staticmethod
+    def build(selected_indices: torch.Tensor, selected_scores: torch.Tensor,
+              retained_assignment_positions: Sequence[int], missing_assignment_positions: Sequence[int],
+              retained_page_slot_by_expert: torch.Tensor,
+              missing_page_slot_by_expert: torch.Tensor) -> "Qwen3_5MoESplitPageRoute":
+        """split_page_route.rs:20-73, with validate_split_page_route (:107-150) on the host."""
+        n = selected_indices.numel()
+        ret, mis = list(retained_assignment_positions), list(missing_assignment_positions)
+        if (n == 0 or selected_scores.numel() != n or not ret or not mis or len(ret) + len(mis) != n):
+            raise AstroMoeError(_lib.INVALID_ARGUMENT, f"{_SPLIT_OP}: selected indices, scores, and "
+                                "non-empty route sides must cover the same assignments")
+        covered = [False] * n
+        for p in ret + mis:
+            if not 0 <= p < n:
+                raise AstroMoeError(_lib.INVALID_ARGUMENT, f"{_SPLIT_OP}: a route assignment position "
+                                    "exceeds the selected assignment count")
+            if covered[p]:
+                raise AstroMoeError(_lib.INVALID_ARGUMENT, f"{_SPLIT_OP}: a route assignment position "
+                                    "appears more than once")
+            covered[p] = True
+        ids = selected_indices.contiguous().view(torch.int32).reshape(-1)
+        sc = selected_scores.contiguous().view(torch.bfloat16).reshape(-1)
+        sides = []
+        for pos, m in ((ret, retained_page_slot_by_expert), (mis, missing_page_slot_by_expert)):
+            p = torch.tensor(pos, dtype=torch.int32, device=ids.device)
+            side_ids = torch.empty(len(pos), dtype=torch.int32, device=ids.device)
+            side_sc = torch.empty(len(pos), dtype=torch.bfloat16, device=ids.device)
+            call("astro_moe_gather_assignments", _ptr(ids), _ptr(sc), _ptr(p), len(pos), _ptr(side_ids),
+                 _ptr(side_sc), _stream(ids.device))
+            sides += [qwen3_5_moe_remap_expert_page_slots(side_ids, m), side_sc]
+        return Qwen3_5MoESplitPageRoute(*sides)
+
+
+def forward_moe_split_paged(hidden_states: torch.Tensor, weights: MoeLayerWeights,
+                            retained_page: MoeLayerWeights, missing_page: MoeLayerWeights,
+                            selected_indices: torch.Tensor, selected_scores: torch.Tensor,
+                            retained_assignment_positions: Sequence[int],
+                            missing_assignment_positions: Sequence[int]) -> torch.Tensor:
+    """forward_moe_split_paged_with_performance_attribution (paged_execution.rs:147-205) for
+    one decode token: the retained and missing pages each run the streamed sparse graph over
+    their side of the route, the partial outputs are added, then the shared expert of
+    `weights` and the shared combine.  Pages carry their slot maps in slot_of_expert."""
+    route = Qwen3_5MoESplitPageRoute.build(
+        selected_indices, selected_scores, retained_assignment_positions, missing_assignment_positions,
+        retained_page.slot_of_expert, missing_page.slot_of_expert)
+    x2 = hidden_states.contiguous().view(torch.bfloat16).reshape(-1, weights.hidden)
+    retained = forward_moe_with_streamed_weights(x2, retained_page, route.retained_page_slot_indices.reshape(1, -1),
+                                                 route.retained_scores.reshape(1, -1))
+    missing = forward_moe_with_streamed_weights(x2, missing_page, route.missing_page_slot_indices.reshape(1, -1),
+                                                route.missing_scores.reshape(1, -1))
+    sparse = add(retained, missing)
+    if not weights.shared_intermediate:
+        return sparse
+    so, z = shared_expert(weights, x2)
+    return combine_sparse_and_shared_experts(sparse, so, z)

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ASTRO_MOE_ABI_VERSION 1
+#define ASTRO_MOE_ABI_VERSION 2
 
 enum astro_moe_status {
   ASTRO_MOE_OK = 0,
@@ -86,7 +86,16 @@ typedef struct astro_moe_layer {
   astro_moe_affine shared_up;
   astro_moe_affine shared_down;         /* [1][H][Is*b/32] */
   astro_moe_affine shared_expert_gate;  /* [1][1][H*b/32] */
-  const uint32_t *slot_of_expert; /* reserved for compact paged pages; must be NULL */
+  /* Compact paged pages (forward_moe_paged_with_performance_attribution,
+   * paged_execution.rs:98-139; page_slot_by_global_expert_id,
+   * quantized_expert_manifest.rs:212-220): when set, u32 [num_experts] maps each global
+   * expert id to its slot in the routed arrays above, whose `experts` is then the page's slot
+   * count; 0xffffffff marks an expert the page does not hold.  Routing is unchanged; the
+   * assignments are sorted and computed by slot.  The reference refuses a routed expert absent
+   * from the page on the host; here each one counts into the workspace word
+   * astro_moe_workspace_view.missing_slots (read it after the stream completes) and reads
+   * slot 0.  NULL: resident arrays indexed by expert id. */
+  const uint32_t *slot_of_expert;
 } astro_moe_layer;
 
 /* Byte offsets of the block's intermediates inside the workspace, valid after
@@ -108,6 +117,8 @@ typedef struct astro_moe_workspace_view {
   size_t sparse;             /* bf16 [T][H] */
   size_t shared_out;         /* bf16 [T][H] */
   size_t shared_gate_logits; /* bf16 [T] */
+  size_t expert_slots;       /* u32 [T][k] page slots (slot_of_expert set; else 0) */
+  size_t missing_slots;      /* u32: routed experts absent from the page (slot_of_expert set) */
 } astro_moe_workspace_view;
 
 const char *astro_moe_last_error(void);
@@ -216,6 +227,48 @@ int astro_moe_shared_expert_workspace_bytes(const astro_moe_layer *layer, int32_
 int astro_moe_shared_expert(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
                             uint16_t *shared_out, uint16_t *gate_logits, void *workspace,
                             size_t workspace_bytes, void *stream);
+
+/*
+ * Paged callers (paged_execution.rs; split_page_route.rs).  The resident block above takes
+ * compact pages through slot_of_expert.  A split-page decode step (retained page + miss page,
+ * forward_moe_split_paged_with_performance_attribution, paged_execution.rs:147-205) composes:
+ *   for each side: astro_moe_gather_assignments (its positions) -> astro_moe_remap_expert_slots
+ *   (its page map) -> astro_moe_streamed_sparse_forward (its page, T = 1, per_token = the
+ *   side's assignment count); then astro_moe_add of the two partial outputs,
+ *   astro_moe_shared_expert and astro_moe_combine_shared.
+ */
+
+/* qwen3_5_moe_remap_expert_page_slots (split_page_route.rs:79-105): slots[a] =
+ * slot_of_expert[expert_ids[a]], a < n.  The reference rejects a routed expert absent from
+ * the page (slot 0xffffffff) on the host; here each absent or out-of-range id adds 1 to
+ * *missing_count (a device word the caller zeroes first; may be NULL) and maps to slot 0, so
+ * every later access stays inside the page. */
+int astro_moe_remap_expert_slots(const uint32_t *expert_ids, int32_t n, const uint32_t *slot_of_expert,
+                                 int32_t experts, uint32_t *slots, uint32_t *missing_count, void *stream);
+
+/* The take of one route side in Qwen3_5MoESplitPageRoute::build (split_page_route.rs:28-55):
+ * out_ids[i] = ids[positions[i]], out_scores[i] = scores[positions[i]], i < n (either output
+ * may be NULL).  validate_split_page_route (split_page_route.rs:107-150) stays with the
+ * caller, which holds the positions on the host. */
+int astro_moe_gather_assignments(const uint32_t *ids, const uint16_t *scores, const uint32_t *positions,
+                                 int32_t n, uint32_t *out_ids, uint16_t *out_scores, void *stream);
+
+/* forward_moe_with_streamed_weights (paged_execution.rs:207-281): the sparse expert output
+ * [T][H] of T tokens with per_token assignments each -- page slots u32 [T][per_token], scores
+ * bf16 [T][per_token] -- against the routed arrays of `page` (gate_up or gate/up, and down;
+ * `experts` = the page's slots; hidden and intermediate set; router, shared expert and
+ * slot_of_expert are not read).  Sorted by slot with the sorted rounding iff
+ * T * per_token >= 64 (routing.rs:13), else the unsorted rounding. */
+int astro_moe_streamed_sparse_workspace_bytes(const astro_moe_layer *page, int32_t tokens,
+                                              int32_t per_token, size_t *bytes);
+int astro_moe_streamed_sparse_forward(const astro_moe_layer *page, const uint16_t *x, int32_t tokens,
+                                      const uint32_t *slots, const uint16_t *scores, int32_t per_token,
+                                      uint16_t *sparse, void *workspace, size_t workspace_bytes,
+                                      void *stream);
+
+/* MlxRuntime::add of the two partial sparse outputs (paged_execution.rs:189-191):
+ * out = bf16(float(a) + float(b)), round to nearest even. */
+int astro_moe_add(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, void *stream);
 
 /*
  * Seeded synthetic inputs for benchmarks and tests (no counterpart in the reference):

@@ -284,3 +284,94 @@ def moe_block_forward(L, x, logits_override=None, trace=False):
         bufs["used_sorted_path"] = bool(tr.used_sorted_path)
         return y, bufs
     return y
+
+
+# ------------------------------------------------------------------- paged callers
+# Compositions of the stage functions above, restating the reference's paged graphs.
+
+SLOT_ABSENT = 0xFFFFFFFF
+
+
+def remap_expert_page_slots(ids, page_slot_by_global_expert_id):
+    """qwen3_5_moe_remap_expert_page_slots (split_page_route.rs:79-105): slots = take(map, ids),
+    refused when a routed expert has no slot (or lies past the map)."""
+    ids = _c(ids, np.uint32)
+    m = _c(page_slot_by_global_expert_id, np.uint32).reshape(-1)
+    if np.any(ids >= m.shape[0]) or np.any(m[np.minimum(ids, m.shape[0] - 1)] == SLOT_ABSENT):
+        raise OracleError(5, "remap expert page slots: a routed expert is absent from the streamed page manifest")
+    return m[ids]
+
+
+def add_bf16(a, b):
+    """MLX add of two bf16 arrays: the fp32 sum rounded to nearest even."""
+    f = (bf16_to_f32(a) + bf16_to_f32(b)).astype(np.float32)
+    return f32_to_bf16(f)
+
+
+def bf16_to_f32(h):
+    return (_c(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f):
+    """Round-to-nearest-even of fp32 to bf16 bit patterns (quiet NaN for NaN inputs)."""
+    u = np.ascontiguousarray(f, dtype=np.float32).view(np.uint32)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def streamed_sparse_forward(x, gate, up, down, slots, scores):
+    """forward_moe_with_streamed_weights (paged_execution.rs:207-281) for T tokens with kk
+    assignments each: slots / scores [T, kk] (page slots, bf16 scores); gate, up, down are the
+    page's arrays (slot-indexed AffineWeights).  Sorted by slot iff T*kk >= 64 (routing.rs:13,
+    sort_expert_assignments over the page's slot count), then up, gate, SwiGLU, down and the
+    sorted or unsorted weighted sum.  Returns the sparse output bf16 [T, H]."""
+    slots = _c(slots, np.uint32)
+    scores = _c(scores, np.uint16)
+    T, kk = scores.shape
+    A = T * kk
+    flat = slots.reshape(-1)
+    rows = np.repeat(np.arange(T, dtype=np.uint32), kk)  # assignment a reads token a // kk
+    capacity = int(np.asarray(down.w).shape[0])
+    if A >= 64:
+        so, inv, sid, _ = sort_assignments(flat, capacity)
+        ids, x_rows = sid, rows[so]
+    else:
+        inv, ids, x_rows = None, flat, rows
+    up_out = gather_qmm(x, up, ids, x_rows=x_rows)
+    gate_out = gather_qmm(x, gate, ids, x_rows=x_rows)
+    act = swiglu(gate_out, up_out)
+    out = gather_qmm(act, down, ids)
+    if A >= 64:
+        return sorted_weighted_sum(out, inv, scores)
+    return unsorted_weighted_sum(out.reshape(T, kk, -1), scores)
+
+
+def paged_shared_combine(L, x, sparse):
+    """combine_paged_sparse_and_shared_outputs (paged_execution.rs:337-374): the shared
+    expert of L on x, then the shared combine (sparse unchanged without a shared expert)."""
+    if not L.shared_intermediate:
+        return _c(sparse, np.uint16)
+    g = qmm(x, L.shared_gate)
+    u = qmm(x, L.shared_up)
+    o = qmm(swiglu(g, u), L.shared_down)
+    z = qmm(x, L.shared_expert_gate).reshape(-1)
+    return combine_shared(sparse, o, z)
+
+
+def split_paged_forward(L, x, indices, scores, retained_positions, missing_positions,
+                        retained_page, retained_map, missing_page, missing_map):
+    """forward_moe_split_paged_with_performance_attribution (paged_execution.rs:147-205) for
+    one decode token: each side takes its assignment positions (split_page_route.rs:28-55),
+    remaps them to its page's slots and runs the streamed sparse graph; the two partial
+    outputs are added in bf16, then the shared combine.  Pages are (gate, up, down)."""
+    ids = _c(indices, np.uint32).reshape(-1)
+    sc = _c(scores, np.uint16).reshape(-1)
+    parts = []
+    for pos, page, m in ((retained_positions, retained_page, retained_map),
+                         (missing_positions, missing_page, missing_map)):
+        pos = np.asarray(pos, dtype=np.int64)
+        slots = remap_expert_page_slots(ids[pos], m)
+        parts.append(streamed_sparse_forward(x, page[0], page[1], page[2], slots.reshape(1, -1),
+                                             sc[pos].reshape(1, -1)))
+    return paged_shared_combine(L, x, add_bf16(parts[0], parts[1]))
