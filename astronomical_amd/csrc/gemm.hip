@@ -16,6 +16,7 @@
 #include "kernels.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace astro {
 
@@ -339,22 +340,24 @@ __device__ __forceinline__ u32x4 dequant8_q4(uint32_t w, float s, float b) {
 // ---------------------------------------------------------------- warp-specialised GEMM
 //
 // 4-bit affine weights, K a multiple of 64, groups of >= 32 inputs (an even number per
-// row).  A workgroup of 8 waves owns one tile of up to 128 rows of one expert and 256
+// row).  A workgroup of 12 waves owns one tile of up to 128 rows of one expert and 256
 // weight rows (plain: 256 output columns; SwiGLU: 128 activated columns = 128 gate + 128
 // up rows), stepping K by 64.  The waves specialise:
-//   - producers (waves 0-3) issue the direct global->LDS loads of the activation tile, the
-//     codes and the scales / biases two steps ahead, and turn step k+1's codes into a bf16
-//     weight tile in LDS (thread t: weight row t, 64 inputs);
-//   - consumers (waves 4-7) run the MFMAs of step k: wave 4 + w owns weight rows
-//     64 w .. +64 and every row block of the tile.
+//   - producers (waves 0-7; wave w owns weight rows 32 w .. +32, two lanes per row) issue
+//     the direct global->LDS loads of the activation tile, the codes and the scales /
+//     biases two steps ahead, and turn step k+1's codes into a bf16 weight tile in LDS
+//     (lane l: weight row 32 w + l / 2, inputs 32 (l % 2) .. +32 of the step);
+//   - consumers (waves 8-11) run the MFMAs of step k: wave 8 + c owns weight rows
+//     64 c .. +64 and every row block of the tile.
 // One s_barrier per step separates the roles' uses of the rings (A, codes, scales: 3 slots;
-// bf16 weights: 2 slots), so each SIMD runs a producer's dequantisation next to a
-// consumer's MFMAs.  Producers wait for their own loads with explicit vmcnt counts; no
+// bf16 weights: 2 slots), so each SIMD runs two producers' dequantisation (two waves issue
+// VALU work at twice the rate of one) next to a consumer's MFMAs.  Producers wait for their own loads with explicit vmcnt counts; no
 // register loads happen inside the loop, so the compiler adds no waits of its own.
 // LDS rows are 128 B (64 bf16) with 16-B chunk c of row r at position c ^ ((r >> 1) & 7),
 // which spreads the 16 rows of an MFMA fragment over all 64 banks.
 constexpr int WK = 64;                         // K step
 constexpr int WNB = 256;                       // weight rows per workgroup
+constexpr int WPW = 8;                         // producer waves (32 weight rows each)
 constexpr int WA_SLOT = 128 * WK * 2;          // 16 KB: activation tile
 constexpr int WC_SLOT = WNB * WK / 2;          // 8 KB: 4-bit codes
 constexpr int WS_SLOT = 2 * WNB * 4;           // 2 KB: one dword of scales, one of biases
@@ -364,37 +367,47 @@ constexpr int kWsLds = WOFF_B + 2 * WB_SLOT;   // 142 KB
 
 __device__ __forceinline__ int wswz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
-// consumer: MFMAs of one K step over 4 column blocks and row blocks 0..3, plus 4..7 when the
-// tile has more than 64 rows (one uniform branch per sub-step)
+// consumer: MFMAs of one K step over the wave's 4 column blocks and the tile's first 2 * NB
+// 16-row blocks, in blocks of two row blocks (sub-step 0 then 1, so an accumulator is reused
+// eight MFMAs later).  The step's B fragments are read first; each row-block pair's A
+// fragments are read one pair ahead, so LDS latency hides behind the MFMAs.
+template <int NB>
 __device__ __forceinline__ void ws_mfma_step(const char *as, const char *bs, int cw, int lane,
-                                             bool full, f32x4 (&acc)[8][4]) {
+                                             f32x4 (&acc)[8][4]) {
   const int c16 = lane & 15, kq = lane >> 4;
+  bf16x8 bf[2][4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    bf16x8 bf[4];
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
       const int n = cw * 64 + f * 16 + c16;
-      bf[f] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(bs + n * 128 + 16 * wswz(n, 4 * j + kq)));
+      bf[j][f] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(bs + n * 128 + 16 * wswz(n, 4 * j + kq)));
     }
-    auto rows = [&](int rb) {
-      const int r = rb * 16 + c16;
-      const bf16x8 af = __builtin_bit_cast(bf16x8, *(const u32x4 *)(as + r * 128 + 16 * wswz(r, 4 * j + kq)));
+  bf16x8 fa[2][2][2];  // [buffer][j][row block of the pair]
+  auto read_blk = [&](int blk, int buf) {
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
-        acc[rb][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[f], acc[rb][f], 0, 0, 0);
-    };
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) rows(rb);
-    if (full) {
+      for (int r2 = 0; r2 < 2; ++r2) {
+        const int r = (2 * blk + r2) * 16 + c16;
+        fa[buf][j][r2] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(as + r * 128 + 16 * wswz(r, 4 * j + kq)));
+      }
+  };
+  read_blk(0, 0);
 #pragma unroll
-      for (int rb = 4; rb < 8; ++rb) rows(rb);
+  for (int blk = 0; blk < NB; ++blk) {
+    if (blk + 1 < NB) read_blk(blk + 1, (blk + 1) & 1);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int j = u >> 3, r2 = (u >> 2) & 1, f = u & 3;
+      const int rb = 2 * blk + r2;
+      acc[rb][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[blk & 1][j][r2], bf[j][f], acc[rb][f], 0, 0, 0);
     }
   }
 }
 
 template <int EPI>
-__global__ __launch_bounds__(512) void ws_gemm_kernel(const GemmArgs pa, const GemmArgs pb, int split,
+__global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs pa, const GemmArgs pb, int split,
                                                       int nba, int nbb) {
   extern __shared__ __attribute__((aligned(16))) char ws_lds[];
   typedef __attribute__((address_space(3))) void lds_void;
@@ -406,99 +419,91 @@ __global__ __launch_bounds__(512) void ws_gemm_kernel(const GemmArgs pa, const G
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nk = p.K / WK;
-  const bool producer = wave < 4;
+  const bool producer = wave < WPW;
 
   if (producer) {
-    // ---- this thread's weight row t = tid (0..255)
-    const int t = tid;
-    int n;
-    bool upper = false;
-    if (EPI == kEpiSwiglu) {
-      // consumer block t / 64 holds 32 gate rows then the 32 up rows of the same columns
-      upper = (t & 63) >= 32;
-      n = nblk * (WNB / 2) + (t >> 6) * 32 + (t & 31);
-    } else {
-      n = nblk * WNB + t;
-    }
-    const int nc = n < p.N ? n : p.N - 1;  // rows past N load a valid row; never stored
-    const uint32_t *wrow = (upper ? p.w1 : p.w0) + (int64_t)expert * p.w_expert_stride + (int64_t)nc * p.w_row_stride;
-    const int64_t so = (int64_t)expert * p.sb_expert_stride + (int64_t)nc * p.sb_row_stride;
-    const uint16_t *srow = (upper ? p.s1 : p.s0) + so;
-    const uint16_t *brow = (upper ? p.b1 : p.b0) + so;
-    // ---- A rows: load v of producer wave w fills rows (v * 4 + w) * 8 + lane / 8, position
+    // ---- this lane's weight row t and half hf (inputs 32 hf .. +32 of each step)
+    const int t = wave * 32 + (lane >> 1), hf = lane & 1;
+    // SwiGLU: consumer block t / 64 holds 32 gate rows (even producer wave) then the 32 up
+    // rows of the same columns (odd producer wave)
+    const bool upper = EPI == kEpiSwiglu && (wave & 1);
+    auto row_of = [&](int tt) {
+      const int n = EPI == kEpiSwiglu ? nblk * (WNB / 2) + (tt >> 6) * 32 + (tt & 31) : nblk * WNB + tt;
+      return n < p.N ? n : p.N - 1;  // rows past N load a valid row; never stored
+    };
+    const uint32_t *wrow = (upper ? p.w1 : p.w0) + (int64_t)expert * p.w_expert_stride +
+                           (int64_t)row_of(t) * p.w_row_stride + 4 * hf;
+    // scale / bias loads: lane l < 32 fetches the scale dword of row 32 w + l, lane 32 + l
+    // the bias dword of the same row
+    const int64_t so = (int64_t)expert * p.sb_expert_stride + (int64_t)row_of(wave * 32 + (lane & 31)) * p.sb_row_stride;
+    const uint16_t *sbrow = (lane < 32 ? (upper ? p.s1 : p.s0) : (upper ? p.b1 : p.b0)) + so;
+    // ---- A rows: load v of producer wave w fills rows (v * WPW + w) * 8 + lane / 8, position
     // lane % 8 (holding K chunk wswz(row, lane % 8))
-    const uint16_t *asrc[4];
+    constexpr int AV = 16 / WPW;
+    const uint16_t *asrc[AV];
     {
-      int src[4];
+      int src[AV];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int r = (v * 4 + wave) * 8 + (lane >> 3);
+      for (int v = 0; v < AV; ++v) {
+        const int r = (v * WPW + wave) * 8 + (lane >> 3);
         src[v] = row0 + (r < m_valid ? r : 0);
       }
       if (p.a_rows) {
-        uint32_t tt[4];
+        uint32_t tt[AV];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) tt[v] = p.a_rows[src[v]];
+        for (int v = 0; v < AV; ++v) tt[v] = p.a_rows[src[v]];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) src[v] = (int)(tt[v] / (uint32_t)p.a_div);
+        for (int v = 0; v < AV; ++v) src[v] = (int)(tt[v] / (uint32_t)p.a_div);
       }
       if (p.a_rows2) {
-        uint32_t tt[4];
+        uint32_t tt[AV];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) tt[v] = p.a_rows2[src[v]];
+        for (int v = 0; v < AV; ++v) tt[v] = p.a_rows2[src[v]];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) src[v] = (int)tt[v];
+        for (int v = 0; v < AV; ++v) src[v] = (int)tt[v];
       }
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int r = (v * 4 + wave) * 8 + (lane >> 3);
+      for (int v = 0; v < AV; ++v) {
+        const int r = (v * WPW + wave) * 8 + (lane >> 3);
         asrc[v] = p.A + (int64_t)src[v] * p.lda + 8 * wswz(r, lane & 7);
       }
     }
-    // group of each half of the step (32 inputs), as dword index / half within the dword
-    auto issue_a = [&](int k) {  // 4 loads
+    auto issue_a = [&](int k) {  // AV loads
       const int kc = k < nk ? k : nk - 1;
       char *base = ws_lds + (k % 3) * WA_SLOT;
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
+      for (int v = 0; v < AV; ++v)
         __builtin_amdgcn_global_load_lds((const void *)(asrc[v] + kc * WK),
-                                         (lds_void *)(base + (v * 4 + wave) * 1024), 16, 0, 0);
+                                         (lds_void *)(base + (v * WPW + wave) * 1024), 16, 0, 0);
     };
-    auto issue_c = [&](int k) {  // 4 loads: codes (2 x 16 B), the scale and the bias dword
+    auto issue_c = [&](int k) {  // 2 loads: codes (16 B per lane), the scale / bias dwords
       const int kc = k < nk ? k : nk - 1;
       const int k0 = kc * WK;
       char *cb = ws_lds + WOFF_C + (k % 3) * WC_SLOT;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        __builtin_amdgcn_global_load_lds((const void *)(wrow + k0 / 8 + 4 * h),
-                                         (lds_void *)(cb + (h * 4 + wave) * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(wrow + k0 / 8), (lds_void *)(cb + wave * 1024), 16, 0, 0);
       const int gd = (k0 / p.group) & ~1;  // dword holding the step's first group
       char *sb = ws_lds + WOFF_S + (k % 3) * WS_SLOT;
-      __builtin_amdgcn_global_load_lds((const void *)(srow + gd), (lds_void *)(sb + wave * 256), 4, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void *)(brow + gd), (lds_void *)(sb + 1024 + wave * 256), 4, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(sbrow + gd), (lds_void *)(sb + wave * 256), 4, 0, 0);
     };
     auto dequant = [&](int k) {  // codes of step k -> bf16 slot k % 2
       const char *cb = ws_lds + WOFF_C + (k % 3) * WC_SLOT;
       const char *sb = ws_lds + WOFF_S + (k % 3) * WS_SLOT;
-      const uint32_t sw = *(const uint32_t *)(sb + wave * 256 + lane * 4);
-      const uint32_t bw = *(const uint32_t *)(sb + 1024 + wave * 256 + lane * 4);
+      const uint32_t sw = *(const uint32_t *)(sb + wave * 256 + (lane >> 1) * 4);
+      const uint32_t bw = *(const uint32_t *)(sb + wave * 256 + 128 + (lane >> 1) * 4);
+      const u32x4 q = *(const u32x4 *)(cb + wave * 1024 + lane * 16);
       const int k0 = k * WK;
+      // group of inputs k0 + 32 hf .. +32, relative to the dword's first group
+      const int gi = (k0 + 32 * hf) / p.group - ((k0 / p.group) & ~1);
+      const float sc = gi ? bf_hi(sw) : bf_lo(sw);
+      const float bi = gi ? bf_hi(bw) : bf_lo(bw);
       char *bs = ws_lds + WOFF_B + (k & 1) * WB_SLOT;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const u32x4 q = *(const u32x4 *)(cb + (h * 4 + wave) * 1024 + lane * 16);
-        // group of inputs k0 + 32 h .. +32, relative to the dword's first group
-        const int gi = (k0 + 32 * h) / p.group - ((k0 / p.group) & ~1);
-        const float sc = gi ? bf_hi(sw) : bf_lo(sw);
-        const float bi = gi ? bf_hi(bw) : bf_lo(bw);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const int c = h * 4 + w;  // 16-B chunk of the row: inputs 8c .. 8c+7
-          *(u32x4 *)(bs + t * 128 + 16 * wswz(t, c)) = dequant8_q4(q[w], sc, bi);
-        }
+      for (int w = 0; w < 4; ++w) {
+        const int c = hf * 4 + w;  // 16-B chunk of the row: inputs 8c .. 8c+7
+        *(u32x4 *)(bs + t * 128 + 16 * wswz(t, c)) = dequant8_q4(q[w], sc, bi);
       }
     };
-    constexpr int NA = 4, NC = 4;
+    constexpr int NA = AV, NC = 2;
     // prologue: codes 0, then [A 0, codes 1], [A 1, codes 2]
     issue_c(0);
     issue_a(0);
@@ -523,7 +528,7 @@ __global__ __launch_bounds__(512) void ws_gemm_kernel(const GemmArgs pa, const G
   }
 
   // ---- consumers
-  const int cw = wave - 4;
+  const int cw = wave - WPW;
   f32x4 acc[8][4];
 #pragma unroll
   for (int rb = 0; rb < 8; ++rb)
@@ -531,12 +536,17 @@ __global__ __launch_bounds__(512) void ws_gemm_kernel(const GemmArgs pa, const G
     for (int f = 0; f < 4; ++f) acc[rb][f] = f32x4{0.f, 0.f, 0.f, 0.f};
   ring_barrier();  // step 0's A and weights are ready
   const bool small = m_valid <= 64;
-  for (int k = 0; k < nk; ++k) {
-    const char *as = ws_lds + (k % 3) * WA_SLOT;
-    const char *bs = ws_lds + WOFF_B + (k & 1) * WB_SLOT;
-    ws_mfma_step(as, bs, cw, lane, !small, acc);
-    ring_barrier();
-  }
+  auto consume = [&](auto nb_tag) {
+    constexpr int NB = decltype(nb_tag)::value;
+    for (int k = 0; k < nk; ++k) {
+      const char *as = ws_lds + (k % 3) * WA_SLOT;
+      const char *bs = ws_lds + WOFF_B + (k & 1) * WB_SLOT;
+      ws_mfma_step<NB>(as, bs, cw, lane, acc);
+      ring_barrier();
+    }
+  };
+  if (small) consume(std::integral_constant<int, 2>());
+  else consume(std::integral_constant<int, 4>());
 
   // ---- epilogue: lane holds column (lane & 15) of each block, rows 4 (lane >> 4) + i
   const int c16 = lane & 15, kq = lane >> 4;
@@ -587,7 +597,7 @@ hipError_t launch_ws(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_t 
   if (b) shape(*b, mtb, nbb);
   if (mta + mtb == 0) return hipSuccess;
   const GemmArgs &bb = b ? *b : a;
-  dim3 grid(mta + mtb, std::max(nba, nbb)), block(512);
+  dim3 grid(mta + mtb, std::max(nba, nbb)), block(64 * (WPW + 4));
   static bool raised[3] = {false, false, false};  // > 64 KB of LDS is an opt-in per kernel
   auto launch = [&](auto kernel, int which) {
     if (!raised[which]) {
