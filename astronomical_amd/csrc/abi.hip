@@ -698,6 +698,7 @@ static size_t sort_ws_bytes(int A, int E) {
 int astro_moe_sort_workspace_bytes(int32_t assignments, int32_t experts, size_t *bytes) {
   if (assignments < 0 || experts <= 0 || !bytes)
     return fail(ASTRO_MOE_INVALID_ARGUMENT, kSortOp, "expert assignments and expanded hidden states have invalid shapes");
+  if (experts > 1024) return fail(ASTRO_MOE_UNSUPPORTED, kSortOp, "the sort kernels support at most 1024 experts");
   *bytes = sort_ws_bytes(assignments, experts);
   return ok();
 }
@@ -708,6 +709,7 @@ int astro_moe_sort_assignments(const uint32_t *ids, int32_t assignments, int32_t
                                size_t workspace_bytes, void *stream) {
   if (assignments < 0 || experts <= 0)
     return fail(ASTRO_MOE_INVALID_ARGUMENT, kSortOp, "expert assignments and expanded hidden states have invalid shapes");
+  if (experts > 1024) return fail(ASTRO_MOE_UNSUPPORTED, kSortOp, "the sort kernels support at most 1024 experts");
   const size_t need = sort_ws_bytes(assignments, experts);
   if (!workspace || workspace_bytes < need) return workspace_fail(kSortOp, need, workspace ? workspace_bytes : 0);
   if (assignments > 0 && (!ids || !sorted_order || !inverse_order || !sorted_ids))

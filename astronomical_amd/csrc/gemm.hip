@@ -468,12 +468,12 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
         asrc[v] = p.A + (int64_t)src[v] * p.lda + 8 * wswz(r, lane & 7);
       }
     }
-    auto issue_a = [&](int k) {  // AV loads
+    auto issue_a = [&](int k, int nav) {  // nav (a constant at each call) loads
       const int kc = k < nk ? k : nk - 1;
       char *base = ws_lds + (k % 3) * WA_SLOT;
 #pragma unroll
       for (int v = 0; v < AV; ++v)
-        __builtin_amdgcn_global_load_lds((const void *)(asrc[v] + kc * WK),
+        if (v < nav) __builtin_amdgcn_global_load_lds((const void *)(asrc[v] + kc * WK),
                                          (lds_void *)(base + (v * WPW + wave) * 1024), 16, 0, 0);
     };
     auto issue_c = [&](int k) {  // 2 loads: codes (16 B per lane), the scale / bias dwords
@@ -503,26 +503,32 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
         *(u32x4 *)(bs + t * 128 + 16 * wswz(t, c)) = dequant8_q4(q[w], sc, bi);
       }
     };
-    constexpr int NA = AV, NC = 2;
-    // prologue: codes 0, then [A 0, codes 1], [A 1, codes 2]
-    issue_c(0);
-    issue_a(0);
-    issue_c(1);
-    issue_a(1);
-    issue_c(2);
-    wait_vmcnt_le(2 * (NA + NC));  // codes 0
-    dequant(0);
-    wait_vmcnt_le(NA + 2 * NC);    // A 0
-    ring_barrier();
-    for (int k = 0; k < nk; ++k) {
-      // step k: the consumers compute step k
-      wait_vmcnt_le(NA + NC);       // codes k + 1
-      if (k + 1 < nk) dequant(k + 1);
-      issue_a(k + 2);
-      issue_c(k + 3);
-      wait_vmcnt_le(NA + 2 * NC);   // A k + 1
+    // NA activation loads per step: a tile of at most 64 rows loads only rows 0-63 (load 0
+    // of every producer wave), the rows its consumers read
+    auto run = [&](auto na_tag) {
+      constexpr int NA = decltype(na_tag)::value, NC = 2;
+      // prologue: codes 0, then [A 0, codes 1], [A 1, codes 2]
+      issue_c(0);
+      issue_a(0, NA);
+      issue_c(1);
+      issue_a(1, NA);
+      issue_c(2);
+      wait_vmcnt_le(2 * (NA + NC));  // codes 0
+      dequant(0);
+      wait_vmcnt_le(NA + 2 * NC);    // A 0
       ring_barrier();
-    }
+      for (int k = 0; k < nk; ++k) {
+        // step k: the consumers compute step k
+        wait_vmcnt_le(NA + NC);       // codes k + 1
+        if (k + 1 < nk) dequant(k + 1);
+        issue_a(k + 2, NA);
+        issue_c(k + 3);
+        wait_vmcnt_le(NA + 2 * NC);   // A k + 1
+        ring_barrier();
+      }
+    };
+    if (m_valid <= 64) run(std::integral_constant<int, 1>());
+    else run(std::integral_constant<int, AV>());
     __builtin_amdgcn_s_waitcnt(0x0f70);  // drain the clamped trailing loads
     return;
   }

@@ -26,33 +26,42 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restr
   }
 }
 
-constexpr int kChunk = 1024;  // assignments per rank / scatter workgroup (16 waves)
+constexpr int kChunk = 1024;  // assignments per rank / place workgroup (16 waves)
+constexpr int kMaxBuckets = 1025;  // experts <= 1024, plus the bucket of ids >= E
 
-// Stable counting sort in three launches.
+// Lanes of this wave whose bucket equals this lane's (invalid lanes match nothing): one
+// ballot per bit of the bucket number.
+__device__ __forceinline__ uint64_t same_bucket_lanes(uint32_t b, bool valid, int nbits) {
+  uint64_t m = __ballot(valid);
+  for (int i = 0; i < nbits; ++i) {
+    const bool bit = (b >> i) & 1u;
+    const uint64_t bal = __ballot(valid && bit);
+    m &= bit ? bal : ~bal;
+  }
+  return m;
+}
+
+// Stable counting sort in two launches.
 // rank: each workgroup takes kChunk consecutive assignments; every wave ranks its 64 ids
-// (number of earlier lanes with the same bucket, from 64 readlanes) and records, per
-// bucket, its count; the workgroup then turns those into chunk-local ranks (earlier waves'
-// counts + the in-wave rank) and writes the chunk's bucket histogram.
+// (number of earlier lanes with the same bucket) and records, per bucket, its count; the
+// workgroup then turns those into chunk-local ranks (earlier waves' counts + the in-wave
+// rank) and writes the chunk's bucket histogram.
 __global__ __launch_bounds__(kChunk) void sort_rank_kernel(const uint32_t *__restrict__ ids, int A,
-                                                           int E, uint32_t *__restrict__ hist,
+                                                           int E, int nbits, uint32_t *__restrict__ hist,
                                                            uint32_t *__restrict__ local_rank) {
   extern __shared__ uint16_t wcnt[];  // [16 waves][E + 1] (a wave counts at most 64)
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int nb = E + 1;
   for (int i = threadIdx.x; i < 16 * nb; i += kChunk) wcnt[i] = 0;
-  __syncthreads();
   const int a = blockIdx.x * kChunk + threadIdx.x;
   const bool valid = a < A;
   const uint32_t id = valid ? ids[a] : 0u;
-  const uint32_t b = !valid ? 0xffffffffu : id < (uint32_t)E ? id : (uint32_t)E;
-  uint32_t before = 0, after = 0;
-#pragma unroll 16
-  for (int l = 0; l < 64; ++l) {
-    const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)b, l);
-    before += (o == b) & (l < lane);
-    after += (o == b) & (l > lane);
-  }
-  if (valid && after == 0) wcnt[w * nb + b] = (uint16_t)(before + 1);  // this lane closes its bucket
+  const uint32_t b = id < (uint32_t)E ? id : (uint32_t)E;
+  const uint64_t m = same_bucket_lanes(b, valid, nbits);
+  const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  const bool closes = (m >> lane) == 1ull;  // no later lane shares the bucket
+  __syncthreads();
+  if (valid && closes) wcnt[w * nb + b] = (uint16_t)(before + 1);
   __syncthreads();
   if (valid) {
     uint32_t r = before;
@@ -67,31 +76,49 @@ __global__ __launch_bounds__(kChunk) void sort_rank_kernel(const uint32_t *__res
   }
 }
 
-// scan: one workgroup.  offsets[e] = sum of earlier buckets (E + 2 entries), base of
-// (chunk, bucket) = offsets[bucket] + that bucket's count in earlier chunks (in place in
-// hist), and the tile table (tiles of kGemmBM rows, experts ascending).
-constexpr int kScanThreads = 1024;
-__global__ __launch_bounds__(kScanThreads) void sort_scan_kernel(
-    uint32_t *__restrict__ hist, int nchunks, int A, int E, uint32_t *__restrict__ offsets,
-    uint32_t *__restrict__ tile_expert, uint32_t *__restrict__ tile_row0,
-    uint32_t *__restrict__ tile_count) {
-  __shared__ uint32_t wsum[2][kScanThreads / 64];
+// place: workgroup c (one per chunk, at least one) sums every chunk's histogram per bucket
+// (total) and the histograms of chunks before c (pre), scans the totals into the bucket
+// offsets, and scatters its chunk to offsets[bucket] + pre[bucket] + local rank.  Workgroup 0
+// also writes offsets (E + 2 entries) and the tile table (tiles of kGemmBM rows, experts
+// ascending).
+__global__ __launch_bounds__(kChunk) void sort_place_kernel(
+    const uint32_t *__restrict__ ids, int A, int E, const uint32_t *__restrict__ hist, int nchunks,
+    const uint32_t *__restrict__ local_rank, uint32_t *__restrict__ sorted_order,
+    uint32_t *__restrict__ inverse_order, uint32_t *__restrict__ sorted_ids,
+    uint32_t *__restrict__ offsets, uint32_t *__restrict__ tile_expert,
+    uint32_t *__restrict__ tile_row0, uint32_t *__restrict__ tile_count) {
+  __shared__ uint32_t base[kMaxBuckets];
+  __shared__ uint32_t wsum[2][kChunk / 64];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int nb = E + 1;
+  const int c = blockIdx.x;
+  const int a = c * kChunk + threadIdx.x;
+  const bool valid = a < A;
+  const uint32_t id = valid ? ids[a] : 0u;
+  const uint32_t lr = valid ? local_rank[a] : 0u;
   // thread e owns bucket e (E + 1 <= 1025 buckets: thread 0 also takes bucket 1024)
-  auto scan_bucket = [&](int e, uint32_t &total, uint32_t &tiles) {
+  auto sums = [&](int e, uint32_t &total, uint32_t &pre) {
     total = 0;
-    tiles = 0;
-    if (e < nb) {
-      for (int c = 0; c < nchunks; ++c) total += hist[(size_t)c * nb + e];
-      if (e < E) tiles = (total + kGemmBM - 1) / kGemmBM;
+    pre = 0;
+    if (e >= nb) return;
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+      uint32_t h[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) h[u] = c0 + u < nchunks ? hist[(size_t)(c0 + u) * nb + e] : 0u;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        total += h[u];
+        pre += c0 + u < c ? h[u] : 0u;
+      }
     }
   };
-  uint32_t total, tiles;
-  scan_bucket(threadIdx.x, total, tiles);
-  uint32_t extra_total = 0, extra_tiles = 0;
-  if (threadIdx.x == 0 && nb > kScanThreads) scan_bucket(kScanThreads, extra_total, extra_tiles);
-  // block exclusive scans of total and tiles
+  const int e = threadIdx.x;
+  uint32_t total, pre;
+  sums(e, total, pre);
+  const uint32_t tiles = e < E ? (total + kGemmBM - 1) / kGemmBM : 0u;
+  uint32_t extra_total = 0, extra_pre = 0;
+  if (threadIdx.x == 0 && nb > kChunk) sums(kChunk, extra_total, extra_pre);
+  // block inclusive scans of total and tiles
   uint32_t it = total, ip = tiles;
   for (int off = 1; off < 64; off <<= 1) {
     const uint32_t o = (uint32_t)__shfl_up((int)it, off, kWave);
@@ -112,52 +139,40 @@ __global__ __launch_bounds__(kScanThreads) void sort_scan_kernel(
     bp += wsum[1][v];
   }
   const uint32_t off_e = bt + it - total, tile0 = bp + ip - tiles;
-  const int e = threadIdx.x;
   if (e < nb) {
-    offsets[e] = off_e;
-    uint32_t run = off_e;
-    for (int c = 0; c < nchunks; ++c) {
-      const uint32_t h = hist[(size_t)c * nb + e];
-      hist[(size_t)c * nb + e] = run;
-      run += h;
-    }
-    for (uint32_t i = 0; i < tiles; ++i) {
-      tile_expert[tile0 + i] = (uint32_t)e;
-      tile_row0[tile0 + i] = off_e + i * kGemmBM;
+    base[e] = off_e + pre;
+    if (c == 0) {
+      offsets[e] = off_e;
+      for (uint32_t i = 0; i < tiles; ++i) {
+        tile_expert[tile0 + i] = (uint32_t)e;
+        tile_row0[tile0 + i] = off_e + i * kGemmBM;
+      }
+      if (e == nb - 1) {  // the last bucket's thread knows the totals
+        offsets[nb] = (uint32_t)A;
+        *tile_count = bp + ip;
+      }
     }
   }
-  if (threadIdx.x == 0 && nb > kScanThreads) {
+  if (threadIdx.x == 0 && nb > kChunk) {
     // bucket 1024 (ids >= E when E = 1024): after every other bucket
-    uint32_t run = (uint32_t)A - extra_total;
-    offsets[kScanThreads] = run;
-    for (int c = 0; c < nchunks; ++c) {
-      const uint32_t h = hist[(size_t)c * nb + kScanThreads];
-      hist[(size_t)c * nb + kScanThreads] = run;
-      run += h;
-    }
-  }
-  if (threadIdx.x == kScanThreads - 1 || (int)threadIdx.x == nb - 1) {
-    // the last bucket's thread knows the totals
-    if ((int)threadIdx.x == min(nb, kScanThreads) - 1) {
+    const uint32_t off_x = (uint32_t)A - extra_total;
+    base[kChunk] = off_x + extra_pre;
+    if (c == 0) {
+      uint32_t nt = 0;  // tiles of buckets 0 .. 1023
+      for (int v = 0; v < kChunk / 64; ++v) nt += wsum[1][v];
+      offsets[kChunk] = off_x;
       offsets[nb] = (uint32_t)A;
-      *tile_count = bp + ip;
+      *tile_count = nt;
     }
   }
-}
-
-// scatter: pos = base of (chunk, bucket) + chunk-local rank
-__global__ __launch_bounds__(kChunk) void sort_scatter_kernel(
-    const uint32_t *__restrict__ ids, int A, int E, const uint32_t *__restrict__ base,
-    const uint32_t *__restrict__ local_rank, uint32_t *__restrict__ sorted_order,
-    uint32_t *__restrict__ inverse_order, uint32_t *__restrict__ sorted_ids) {
-  const int a = blockIdx.x * kChunk + threadIdx.x;
-  if (a >= A) return;
-  const uint32_t id = ids[a];
-  const uint32_t b = id < (uint32_t)E ? id : (uint32_t)E;
-  const uint32_t pos = base[(size_t)blockIdx.x * (E + 1) + b] + local_rank[a];
-  sorted_order[pos] = (uint32_t)a;
-  sorted_ids[pos] = id;
-  inverse_order[a] = pos;
+  __syncthreads();
+  if (valid) {
+    const uint32_t b = id < (uint32_t)E ? id : (uint32_t)E;
+    const uint32_t pos = base[b] + lr;
+    sorted_order[pos] = (uint32_t)a;
+    sorted_ids[pos] = id;
+    inverse_order[a] = pos;
+  }
 }
 
 }  // namespace
@@ -200,21 +215,20 @@ hipError_t launch_sort(const uint32_t *ids, int A, int E, uint32_t *sorted_order
                        uint32_t *inverse_order, uint32_t *sorted_ids, uint32_t *offsets,
                        uint32_t *tile_expert, uint32_t *tile_row0, uint32_t *tile_count,
                        uint32_t *scratch, hipStream_t s) {
+  if (E < 1 || E + 1 > kMaxBuckets) return hipErrorInvalidValue;
   const int nchunks = (A + kChunk - 1) / kChunk;
   uint32_t *hist = scratch;
   uint32_t *local_rank = (uint32_t *)((char *)scratch + (((size_t)nchunks * (E + 1) * 4 + 255) & ~(size_t)255));
+  const int nbits = 32 - __builtin_clz((unsigned)E);  // bits of the largest bucket number, E
   if (nchunks > 0) {
     hipLaunchKernelGGL(sort_rank_kernel, dim3(nchunks), dim3(kChunk), sizeof(uint16_t) * 16 * ((size_t)E + 1),
-                       s, ids, A, E, hist, local_rank);
+                       s, ids, A, E, nbits, hist, local_rank);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, hist, nchunks, A, E, offsets,
-                     tile_expert, tile_row0, tile_count);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || A == 0) return err;
-  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nchunks), dim3(kChunk), 0, s, ids, A, E, hist, local_rank,
-                     sorted_order, inverse_order, sorted_ids);
+  hipLaunchKernelGGL(sort_place_kernel, dim3(nchunks > 0 ? nchunks : 1), dim3(kChunk), 0, s, ids, A, E, hist,
+                     nchunks, local_rank, sorted_order, inverse_order, sorted_ids, offsets, tile_expert,
+                     tile_row0, tile_count);
   return hipGetLastError();
 }
 

@@ -54,6 +54,14 @@ def test_route_validation_messages(L):
     assert lib.astro_moe_route_topk(None, 1, 2048, 8, 1, None, None, None) == L.UNSUPPORTED
 
 
+def test_sort_rejects_more_than_1024_experts(L):
+    lib = L.lib()
+    need = C.c_size_t()
+    assert lib.astro_moe_sort_workspace_bytes(16, 1025, C.byref(need)) == L.UNSUPPORTED
+    assert "at most 1024 experts" in lib.astro_moe_last_error().decode()
+    assert lib.astro_moe_sort_workspace_bytes(16, 1024, C.byref(need)) == 0
+
+
 def _affine(bits=4, group=64, E=2, out=8, inp=128):
     from astronomical_amd._lib import Affine
     return Affine(1, 1, 1, E, out, inp, bits, group)  # fake non-null pointers: never dereferenced

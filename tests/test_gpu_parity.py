@@ -82,7 +82,8 @@ def test_route_and_combine_kat(ops, kats):
 
 # ------------------------------------------------------------------ sort
 
-@pytest.mark.parametrize("A,E", [(6, 6), (64, 32), (16384, 256), (32768, 256), (4096, 128), (1, 4)])
+@pytest.mark.parametrize("A,E", [(6, 6), (64, 32), (16384, 256), (32768, 256), (4096, 128), (1, 4),
+                                 (5000, 1024), (2048, 1)])
 def test_sort_bit_exact(ops, orc, A, E):
     rng = np.random.default_rng(A + E)
     if A == 32768:  # skewed: most assignments on a few experts, many experts empty
@@ -95,6 +96,23 @@ def test_sort_bit_exact(ops, orc, A, E):
     assert np.array_equal(_np(r.inverse_order), inv)
     assert np.array_equal(_np(r.sorted_indices), sid)
     assert np.array_equal(_np(r.expert_offsets), off)
+
+
+def test_sort_puts_out_of_range_ids_last(ops):
+    """ids >= E (E = 1024 uses the extra bucket past the workgroup's 1024 threads) sort after
+    every expert, stably; checked against numpy's stable argsort of the clipped ids."""
+    rng = np.random.default_rng(7)
+    E, A = 1024, 6000
+    ids = rng.integers(0, E + 80, size=A).astype(np.uint32)
+    r = ops.sort_expert_assignments(_dev_u32(ids), E)
+    want = np.argsort(np.minimum(ids, E), kind="stable").astype(np.uint32)
+    assert np.array_equal(_np(r.sorted_order), want)
+    assert np.array_equal(_np(r.sorted_indices), ids[want])
+    inv = np.empty(A, np.uint32)
+    inv[want] = np.arange(A, dtype=np.uint32)
+    assert np.array_equal(_np(r.inverse_order), inv)
+    counts = np.bincount(np.minimum(ids, E), minlength=E + 1)
+    assert np.array_equal(_np(r.expert_offsets)[: E + 1], np.concatenate([[0], np.cumsum(counts[:E])]).astype(np.uint32))
 
 
 def test_sort_kat(ops, kats):
