@@ -622,75 +622,82 @@ hipError_t launch_ws(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_t 
 
 // Dense bf16 weights over one implicit group of rows (the router projection at prefill
 // sizes, N = experts is small): a 32-row x 64-column output tile per 4-wave workgroup, so
-// that even N = 256 gives M / 32 * 4 workgroups.  Operands go straight from global memory
-// into MFMA registers: wave w owns columns 16 w .. +16 of the tile and both 16-row blocks,
-// lane (c, q) loading 8 consecutive inputs q * 8 .. +8 of each 32-input step of its row /
-// weight row.  The four waves read the same activation rows (the vector L1 serves the
-// repeats).  K advances 256 at a time; the loads of the next 256 are issued before the
-// MFMAs of the current ones.  Workgroups of one 32-row block share an XCD.
-constexpr int DT_M = 32, DT_N = 64, DT_K = 256, DT_J = DT_K / 32;
+// that even N = 256 gives M / 32 * 4 workgroups.  K advances 128 at a time through 4 LDS
+// stages (96 KB) filled three steps ahead by direct global->LDS loads in which 16
+// consecutive lanes read one row's 256 bytes (a fragment-shaped register load, 16 rows per
+// instruction, keeps the texture addresser busy one lane per cycle).  LDS rows are 256 B
+// with 16-B chunk c of row r at position c ^ (r & 15), so the 16 rows of a fragment read hit
+// 16 different 16-B bank groups; wave w owns columns 16 w .. +16 of the tile and both
+// 16-row blocks.  Workgroups of one 32-row block share an XCD.
+constexpr int DT_M = 32, DT_N = 64, DT_K = 128, DT_STAGES = 4, DT_J = DT_K / 32;
+constexpr int DT_ROW = DT_K * 2;                                          // 256 B
+constexpr int DT_ASLOT = DT_M * DT_ROW, DT_BSLOT = DT_N * DT_ROW;        // 8 KB, 16 KB
+constexpr int DT_SLOT = DT_ASLOT + DT_BSLOT;
+constexpr int kDenseLds = DT_STAGES * DT_SLOT;                            // 96 KB
+constexpr int DT_LOADS = (DT_M + DT_N) * DT_ROW / 1024 / 4;               // per wave per stage: 6
 
-struct DenseFrag {
-  u32x4 a0[DT_J], a1[DT_J], b[DT_J];
-};
-
-__device__ __forceinline__ void dense_load(DenseFrag &f, const uint16_t *a0, const uint16_t *a1,
-                                           const uint16_t *bp, int k0) {
-#pragma unroll
-  for (int j = 0; j < DT_J; ++j) {
-    f.a0[j] = *(const u32x4 *)(a0 + k0 + 32 * j);
-    f.a1[j] = *(const u32x4 *)(a1 + k0 + 32 * j);
-    f.b[j] = *(const u32x4 *)(bp + k0 + 32 * j);
-  }
-}
-
-__device__ __forceinline__ void dense_mfma(const DenseFrag &f, f32x4 &acc0, f32x4 &acc1) {
-#pragma unroll
-  for (int j = 0; j < DT_J; ++j) {
-    const bf16x8 b = __builtin_bit_cast(bf16x8, f.b[j]);
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.a0[j]), b, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.a1[j]), b, acc1, 0, 0, 0);
-  }
-}
+__device__ __forceinline__ int dswz(int r, int c) { return c ^ (r & 15); }
 
 template <int EPI>
 __global__ __launch_bounds__(256) void dense_gemm_kernel(const GemmArgs p, int nrb, int ncb) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  typedef __attribute__((address_space(3))) void lds_void;
   const int blk = blockIdx.x;
   const int rb = (blk & 7) + 8 * (blk / (8 * ncb));
   const int cb = (blk >> 3) % ncb;
   if (rb >= nrb) return;  // grid padding to whole rounds of 8 row blocks
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int c16 = lane & 15, kq = lane >> 4;
-  const int r0 = rb * DT_M + c16, r1 = r0 + 16;
-  const int n = cb * DT_N + wave * 16 + c16;
-  const uint16_t *a0 = p.A + (int64_t)(r0 < p.M ? r0 : p.M - 1) * p.lda + kq * 8;
-  const uint16_t *a1 = p.A + (int64_t)(r1 < p.M ? r1 : p.M - 1) * p.lda + kq * 8;
-  const uint16_t *bp = p.bd + (int64_t)(n < p.N ? n : p.N - 1) * p.bd_row_stride + kq * 8;
-  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  const int kmain = p.K / DT_K * DT_K;
-  if (kmain > 0) {
-    DenseFrag f0, f1;
-    dense_load(f0, a0, a1, bp, 0);
-    // ping-pong over two register sets; the last prefetch re-reads the final chunk
-    for (int k0 = 0; k0 < kmain; k0 += 2 * DT_K) {
-      const int k1 = k0 + DT_K < kmain ? k0 + DT_K : kmain - DT_K;
-      dense_load(f1, a0, a1, bp, k1);
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
-      dense_mfma(f0, acc0, acc1);
-      if (k0 + DT_K >= kmain) break;
-      const int k2 = k0 + 2 * DT_K < kmain ? k0 + 2 * DT_K : kmain - DT_K;
-      dense_load(f0, a0, a1, bp, k2);
-      __builtin_amdgcn_sched_barrier(0);
-      dense_mfma(f1, acc0, acc1);
+  const int nk = p.K / DT_K;
+  // load i of this wave covers tile row 4 (6 wave + i) + lane / 16 of the stage (rows 0-31:
+  // A, rows 32-95: B), LDS position lane % 16 holding chunk dswz(row, lane % 16)
+  const int lr = lane >> 4, lp = lane & 15;
+  const uint16_t *src[DT_LOADS];
+#pragma unroll
+  for (int i = 0; i < DT_LOADS; ++i) {
+    const int tr = 4 * (DT_LOADS * wave + i) + lr;
+    if (tr < DT_M) {
+      const int gr = rb * DT_M + tr;
+      src[i] = p.A + (int64_t)(gr < p.M ? gr : p.M - 1) * p.lda + 8 * dswz(tr, lp);
+    } else {
+      const int n = tr - DT_M, g = cb * DT_N + n;
+      src[i] = p.bd + (int64_t)(g < p.N ? g : p.N - 1) * p.bd_row_stride + 8 * dswz(n, lp);
     }
   }
-  for (int k0 = kmain; k0 < p.K; k0 += 32) {  // K % 256 tail, 32 at a time
-    const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4 *)(bp + k0));
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4 *)(a0 + k0)), b, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4 *)(a1 + k0)), b, acc1, 0, 0, 0);
+  auto issue = [&](int k) {  // stage k (clamped to the last step) into its slot
+    const int kc = (k < nk ? k : nk - 1) * DT_K;
+    char *slot = lds + (k % DT_STAGES) * DT_SLOT;
+#pragma unroll
+    for (int i = 0; i < DT_LOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void *)(src[i] + kc),
+                                       (lds_void *)(slot + (DT_LOADS * wave + i) * 1024), 16, 0, 0);
+  };
+  const int c16 = lane & 15, kq = lane >> 4;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < DT_STAGES - 1; ++k) issue(k);
+  for (int k = 0; k < nk; ++k) {
+    wait_vmcnt_le(DT_LOADS * (DT_STAGES - 2));  // this wave's loads of stage k
+    ring_barrier();  // every wave's loads of stage k are in LDS; stage k - 1 is consumed
+    issue(k + DT_STAGES - 1);
+    const char *as = lds + (k % DT_STAGES) * DT_SLOT, *bs = as + DT_ASLOT;
+    bf16x8 fa[DT_J][2], fb[DT_J];
+    const int n = wave * 16 + c16, r0 = c16, r1 = 16 + c16;
+#pragma unroll
+    for (int j = 0; j < DT_J; ++j) {
+      fb[j] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(bs + n * DT_ROW + 16 * dswz(n, 4 * j + kq)));
+      fa[j][0] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(as + r0 * DT_ROW + 16 * dswz(r0, 4 * j + kq)));
+      fa[j][1] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(as + r1 * DT_ROW + 16 * dswz(r1, 4 * j + kq)));
+    }
+#pragma unroll
+    for (int j = 0; j < DT_J; ++j) {
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[j][0], fb[j], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[j][1], fb[j], acc1, 0, 0, 0);
+    }
   }
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // drain the clamped trailing loads
   // lane holds column c16 of rows 4 kq + i of each 16-row block
+  const int n = cb * DT_N + wave * 16 + c16;
   if (n >= p.N) return;
   const float bias = EPI == kEpiBias ? bf2f(p.bias[n]) : 0.f;
 #pragma unroll
@@ -709,17 +716,25 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(const GemmArgs p, int n
 hipError_t launch_dense(const GemmArgs &a, int epi, hipStream_t s) {
   const int nrb = (a.M + DT_M - 1) / DT_M, ncb = (a.N + DT_N - 1) / DT_N;
   const int grid = ((nrb + 7) & ~7) * ncb;
-  if (epi == kEpiBias)
-    hipLaunchKernelGGL(dense_gemm_kernel<kEpiBias>, dim3(grid), dim3(256), 0, s, a, nrb, ncb);
-  else
-    hipLaunchKernelGGL(dense_gemm_kernel<kEpiPlain>, dim3(grid), dim3(256), 0, s, a, nrb, ncb);
-  return hipGetLastError();
+  static bool raised[2] = {false, false};  // > 64 KB of LDS is an opt-in per kernel
+  auto launch = [&](auto kernel, int which) {
+    if (!raised[which]) {
+      const hipError_t e = hipFuncSetAttribute((const void *)kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kDenseLds);
+      if (e != hipSuccess) return e;
+      raised[which] = true;
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), kDenseLds, s, a, nrb, ncb);
+    return hipGetLastError();
+  };
+  if (epi == kEpiBias) return launch(dense_gemm_kernel<kEpiBias>, 0);
+  return launch(dense_gemm_kernel<kEpiPlain>, 1);
 }
 
 bool use_dense(const GemmArgs &a, int epi) {
-  // one implicit group, bf16 weights, 16-B aligned 32-input steps, no row indirection
+  // one implicit group, bf16 weights, 16-B aligned 64-input steps, no row indirection
   return a.bkind == kBDense && !a.tile_expert && !a.a_rows && !a.c_rows && epi != kEpiSwiglu &&
-         a.K % 32 == 0 && a.lda % 8 == 0 && a.bd_row_stride % 8 == 0 && a.M > 0 && a.N > 0 &&
+         a.K % DT_K == 0 && a.lda % 8 == 0 && a.bd_row_stride % 8 == 0 && a.M > 0 && a.N > 0 &&
          ((uintptr_t)a.A & 15) == 0 && ((uintptr_t)a.bd & 15) == 0;
 }
 
