@@ -337,6 +337,28 @@ __device__ __forceinline__ u32x4 dequant8_q4(uint32_t w, float s, float b) {
   return o;
 }
 
+// 4 words of codes (32 inputs) -> 4 chunks of 8 bf16, the words' conversions interleaved
+// (each byte position converts 8 independent values) so that dependent instructions are
+// several issues apart.
+__device__ __forceinline__ void dequant32_q4(const u32x4 &q, float s, float b, u32x4 (&o)[4]) {
+  uint32_t lo[4], hi[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo[w]) : "v"(q[w]));
+#pragma unroll
+  for (int w = 0; w < 4; ++w) asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi[w]) : "v"(q[w] >> 4));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float f0[4], f1[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      f0[w] = __builtin_fmaf(s, (float)((lo[w] >> (8 * i)) & 255u), b);
+      f1[w] = __builtin_fmaf(s, (float)((hi[w] >> (8 * i)) & 255u), b);
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w][i] = pack_bf2_hw(f0[w], f1[w]);
+  }
+}
+
 // ---------------------------------------------------------------- warp-specialised GEMM
 //
 // 4-bit affine weights, K a multiple of 64, groups of >= 32 inputs (an even number per
@@ -419,6 +441,7 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nk = p.K / WK;
+  const int lgg = __builtin_ctz((unsigned)p.group);  // group size: a power of two >= 32
   const bool producer = wave < WPW;
 
   if (producer) {
@@ -481,7 +504,7 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
       const int k0 = kc * WK;
       char *cb = ws_lds + WOFF_C + (k % 3) * WC_SLOT;
       __builtin_amdgcn_global_load_lds((const void *)(wrow + k0 / 8), (lds_void *)(cb + wave * 1024), 16, 0, 0);
-      const int gd = (k0 / p.group) & ~1;  // dword holding the step's first group
+      const int gd = (k0 >> lgg) & ~1;  // dword holding the step's first group
       char *sb = ws_lds + WOFF_S + (k % 3) * WS_SLOT;
       __builtin_amdgcn_global_load_lds((const void *)(sbrow + gd), (lds_void *)(sb + wave * 256), 4, 0, 0);
     };
@@ -493,14 +516,16 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
       const u32x4 q = *(const u32x4 *)(cb + wave * 1024 + lane * 16);
       const int k0 = k * WK;
       // group of inputs k0 + 32 hf .. +32, relative to the dword's first group
-      const int gi = (k0 + 32 * hf) / p.group - ((k0 / p.group) & ~1);
+      const int gi = ((k0 + 32 * hf) >> lgg) - ((k0 >> lgg) & ~1);
       const float sc = gi ? bf_hi(sw) : bf_lo(sw);
       const float bi = gi ? bf_hi(bw) : bf_lo(bw);
       char *bs = ws_lds + WOFF_B + (k & 1) * WB_SLOT;
+      u32x4 o[4];
+      dequant32_q4(q, sc, bi, o);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const int c = hf * 4 + w;  // 16-B chunk of the row: inputs 8c .. 8c+7
-        *(u32x4 *)(bs + t * 128 + 16 * wswz(t, c)) = dequant8_q4(q[w], sc, bi);
+        *(u32x4 *)(bs + t * 128 + 16 * wswz(t, c)) = o[w];
       }
     };
     // NA activation loads per step: a tile of at most 64 rows loads only rows 0-63 (load 0
@@ -742,7 +767,8 @@ bool use_ws(const GemmArgs &a) {
   // 4-bit weights with K steps of 64 and an even number of groups of >= 32 inputs per row
   // (one dword of scales per step stays 4-byte aligned); K >= 1024: with fewer K steps its
   // two-step prefetch ramp outweighs the gain
-  return a.bkind == kBQ4 && a.K % WK == 0 && a.K >= 1024 && a.group >= 32 && (a.K / a.group) % 2 == 0;
+  return a.bkind == kBQ4 && a.K % WK == 0 && a.K >= 1024 && a.group >= 32 &&
+         (a.group & (a.group - 1)) == 0 && (a.K / a.group) % 2 == 0;
 }
 
 }  // namespace
