@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--layers", type=int, default=40)
     p.add_argument("--prefill-iters", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the side measurements of configs c3 and c4")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--copy-check", action="store_true",
                    help="run a 1 GiB streaming copy first (counter calibration)")
@@ -193,6 +195,9 @@ def main():
     prefill_stage_ms = {kname: statistics.median(v) for kname, v in pst.items()}
     log(f"prefill: {prefill_ms * 1000:.1f} us")
 
+    # ---------------------------------------------------------------- side measurements
+    extra = None if args.no_extra else other_configs(CF, DS, ops, torch, K, W)
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -246,9 +251,84 @@ def main():
             "frac_of_bf16_peak": round(prefill_flops / (prefill_ms * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 4),
             "stage_us": {k_: round(v * 1000, 2) for k_, v in prefill_stage_ms.items()},
         },
+        "other_configs": extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))
+
+
+def other_configs(CF, DS, ops, torch, K, W):
+    """c3 (4096-token prefill with Zipf-skewed routing) and c4 (48 stacked 8-bit layers: decode
+    B=1 through a graph of all 48, and 512-token prefill per layer), timed with events."""
+    out = {}
+
+    def prefill_entry(cfg, T, us):
+        tf = cfg.flops_per_token() * T / (us * 1e-6) / 1e12
+        return {"tokens": T, "us_per_layer": round(us, 1), "tokens_per_s": round(T / (us * 1e-6), 1),
+                "achieved_TFLOPs": round(tf, 2), "frac_of_bf16_peak": round(tf / BF16_DENSE_PEAK_TFLOPS, 4)}
+
+    def time_ms(fn, iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    # c3: skewed routing (router bias 2 ln Zipf(1.1) rank weights), 4096 tokens
+    c3 = CF.C3
+    L3 = DS.make_layer_device(c3, layer=0)
+    b3 = ops.MoeBlock(L3)
+    x3 = DS.make_tokens_device(c3, 4096)
+    y3 = torch.empty_like(x3)
+    ws3 = b3.workspace(4096)
+    ms = time_ms(lambda: b3.forward(x3, out=y3, workspace=ws3), 10)
+    out["c3_prefill"] = dict(workload="c3: c1 shapes, 4096 tokens, Zipf-skewed routing", **prefill_entry(c3, 4096, ms * 1000))
+    del L3, b3, x3, y3, ws3
+
+    # c4: 48 stacked 8-bit layers
+    c4 = CF.C4
+    nL4 = c4.layers
+    L4 = [DS.make_layer_device(c4, layer=l) for l in range(nL4)]
+    b4 = [ops.MoeBlock(L) for L in L4]
+    ws4 = b4[0].workspace(512)
+    t4 = DS.make_tokens_device(c4, nL4, step=1).reshape(nL4, 1, c4.hidden)
+    o4 = torch.empty_like(t4)
+
+    def decode_pass():
+        for l in range(nL4):
+            b4[l].forward(t4[l], out=o4[l], workspace=ws4)
+    decode_pass()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        decode_pass()
+    for _ in range(W):
+        g.replay()
+    ms = time_ms(g.replay, K)
+    us_layer = ms * 1000 / nL4
+    credited = c4.top_k * c4.page_bytes  # 8 distinct routed expert pages, no shared expert
+    gbs = credited / (us_layer * 1e-6) / 1e9
+    out["c4_decode"] = {"workload": f"c4 decode B=1 through a graph of {nL4} distinct 8-bit layers",
+                        "us_per_layer": round(us_layer, 2), "tokens_per_s_48_layers": round(1e6 / (us_layer * nL4), 1),
+                        "credited_bytes_per_layer": int(credited), "achieved_GBps": round(gbs, 1),
+                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    xp = DS.make_tokens_device(c4, 512)
+    yp = torch.empty_like(xp)
+
+    def prefill_pass():
+        for l in range(nL4):
+            b4[l].forward(xp, out=yp, workspace=ws4)
+    ms = time_ms(prefill_pass, 3)
+    out["c4_prefill"] = dict(workload=f"c4: 512 tokens through each of {nL4} 8-bit layers",
+                             **prefill_entry(c4, 512, ms * 1000 / nL4))
+    del L4, b4, ws4
+    torch.cuda.empty_cache()
+    log(f"other configs: {json.dumps(out)}")
+    return out
 
 
 def cpu_baseline(layer_dev, toks, cfg, seconds):
