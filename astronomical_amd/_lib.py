@@ -48,7 +48,41 @@ class WorkspaceView(C.Structure):
                                   "missing_slots")]
 
 
+PATH_MAX = 1024
+DTYPES = ("BOOL", "I8", "U8", "F8_E4M3", "F8_E5M2", "I16", "U16", "F16", "BF16", "I32", "U32",
+          "F32", "I64", "U64")
+
+
+class TensorSource(C.Structure):
+    _fields_ = [("source_file", C.c_char * PATH_MAX), ("dtype", C.c_int32), ("shape", C.c_int64 * 3),
+                ("file_offset", C.c_uint64), ("bytes_per_expert", C.c_uint64), ("file_size", C.c_uint64)]
+
+
+class ExpertLayerPlan(C.Structure):
+    _fields_ = [("src", (TensorSource * 3) * 3), ("expert_capacity", C.c_int32),
+                ("bits", C.c_int32 * 3), ("group_size", C.c_int32 * 3), ("gate_up_fusable", C.c_int32),
+                ("gate_up_separate_reason", C.c_char * 96)]
+
+
+class PageInterval(C.Structure):
+    _fields_ = [("projection", C.c_int32), ("parameter", C.c_int32), ("expert_start", C.c_int32),
+                ("expert_count", C.c_int32), ("first_page_slot", C.c_int32), ("file_offset", C.c_uint64),
+                ("byte_count", C.c_uint64), ("virtual_offset", C.c_uint64)]
+
+
 EXPORTS = {
+    "astro_moe_safetensors_tensor": ([C.c_char_p, C.c_char_p, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
+                                      C.POINTER(C.c_int64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)],
+                                     C.c_int),
+    "astro_moe_build_expert_layer_plan": ([C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p),
+                                           C.c_int32, C.c_char_p, C.POINTER(C.c_int32),
+                                           C.POINTER(C.c_int32), C.POINTER(ExpertLayerPlan)], C.c_int),
+    "astro_moe_build_expert_page_manifest": ([C.POINTER(ExpertLayerPlan), C.POINTER(C.c_int32), C.c_int32,
+                                              C.c_void_p, C.POINTER(PageInterval), C.c_int32,
+                                              C.POINTER(C.c_int32), C.POINTER(C.c_uint64)], C.c_int),
+    "astro_moe_load_expert_page": ([C.POINTER(ExpertLayerPlan), C.POINTER(C.c_int32), C.c_int32, C.c_int32,
+                                    C.POINTER(C.c_void_p), C.c_int32, C.c_void_p, C.c_size_t, C.c_void_p,
+                                    C.POINTER(C.c_uint64)], C.c_int),
     # name: (argtypes, restype)
     "astro_moe_remap_expert_slots": ([C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p,
                                       C.c_void_p, C.c_void_p], C.c_int),

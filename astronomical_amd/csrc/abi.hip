@@ -10,6 +10,7 @@
 
 #include "../../include/astro_moe.h"
 #include "kernels.h"
+#include "status.h"
 
 using namespace astro;
 
@@ -44,6 +45,22 @@ int workspace_fail(const char *op, size_t need, size_t have) {
               "allowed_bytes=%zu",
               need, have);
 }
+
+}  // namespace
+
+int astro::report(int status, const char *op, const char *fmt, ...) {
+  char buf[768];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = std::string(op) + ": " + buf;
+  return status;
+}
+
+int astro::report_ok() { return ok(); }
+
+namespace {
 
 const char *const kBlockOp = "run the Qwen3.5-MoE sparse expert block";
 const char *const kRouteOp = "route Qwen3.5-MoE sparse experts";           // routing.rs:11

@@ -196,7 +196,7 @@ def main():
     log(f"prefill: {prefill_ms * 1000:.1f} us")
 
     # ---------------------------------------------------------------- side measurements
-    extra = None if args.no_extra else other_configs(CF, DS, ops, torch, K, W)
+    extra = None if args.no_extra else other_configs(CF, DS, ops, torch, K, W, layers[0])
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
@@ -257,10 +257,11 @@ def main():
     print(json.dumps(result))
 
 
-def other_configs(CF, DS, ops, torch, K, W):
-    """c3 (4096-token prefill with Zipf-skewed routing) and c4 (48 stacked 8-bit layers: decode
-    B=1 through a graph of all 48, and 512-token prefill per layer), timed with events."""
-    out = {}
+def other_configs(CF, DS, ops, torch, K, W, layer_c1):
+    """c3 (4096-token prefill with Zipf-skewed routing), c4 (48 stacked 8-bit layers: decode
+    B=1 through a graph of all 48, and 512-token prefill per layer), timed with events, and
+    the expert page loader (a c1 decode page from a safetensors checkpoint into HBM)."""
+    out = {"expert_page_load": page_load(CF, torch, layer_c1)}
 
     def prefill_entry(cfg, T, us):
         tf = cfg.flops_per_token() * T / (us * 1e-6) / 1e12
@@ -329,6 +330,46 @@ def other_configs(CF, DS, ops, torch, K, W):
     torch.cuda.empty_cache()
     log(f"other configs: {json.dumps(out)}")
     return out
+
+
+def page_load(CF, torch, L, n_experts=16, ids=(1, 3, 4, 6, 8, 10, 12, 15), reps=5):
+    """Loads 8 experts of a c1-shaped checkpoint (the first 16 experts of layer 0, gate / up /
+    down in two shards) from the page cache into HBM through 64 MiB of pinned staging."""
+    import tempfile
+    from safetensors.torch import save_file
+    from astronomical_amd import pages as PG
+    I = CF.C1.intermediate
+    pre = "model.layers.0.mlp"
+
+    def t(a):  # device int32 / bf16 -> host tensors safetensors writes as U32 / BF16
+        a = a.detach().cpu().contiguous()
+        return a.view(torch.uint32) if a.dtype == torch.int32 else a
+
+    gu, dn = L.gate_up, L.down
+    parts = {"gate_proj": [gu.w[:n_experts, :I], gu.scales[:n_experts, :I], gu.biases[:n_experts, :I]],
+             "up_proj": [gu.w[:n_experts, I:], gu.scales[:n_experts, I:], gu.biases[:n_experts, I:]],
+             "down_proj": [dn.w[:n_experts], dn.scales[:n_experts], dn.biases[:n_experts]]}
+    with tempfile.TemporaryDirectory() as td:
+        wm = {}
+        for shard, projs in (("model-00001-of-00002.safetensors", ["gate_proj"]),
+                             ("model-00002-of-00002.safetensors", ["up_proj", "down_proj"])):
+            tensors = {f"{pre}.switch_mlp.{pj}.{pa}": t(a) for pj in projs
+                       for pa, a in zip(("weight", "scales", "biases"), parts[pj])}
+            save_file(tensors, os.path.join(td, shard))
+            wm.update({k: shard for k in tensors})
+        plan = PG.build_quantized_expert_layer_plan(td, wm, pre, CF.C1.bits, CF.C1.group_size)
+        staging = torch.empty(64 << 20, dtype=torch.uint8).pin_memory()
+        PG.load_quantized_expert_page(plan, ids, "cuda", staging=staging)  # page cache warm
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            page = PG.load_quantized_expert_page(plan, ids, "cuda", staging=staging)
+            times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return {"workload": f"c1 decode page: {len(ids)} of {n_experts} experts (gate, up, down: codes, "
+                        "scales, biases) from a two-shard safetensors checkpoint in the page cache into HBM",
+            "bytes": page.bytes_read, "ms": round(sec * 1e3, 3),
+            "GBps": round(page.bytes_read / sec / 1e9, 2)}
 
 
 def cpu_baseline(layer_dev, toks, cfg, seconds):

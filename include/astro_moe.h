@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ASTRO_MOE_ABI_VERSION 2
+#define ASTRO_MOE_ABI_VERSION 3
 
 enum astro_moe_status {
   ASTRO_MOE_OK = 0,
@@ -269,6 +269,89 @@ int astro_moe_streamed_sparse_forward(const astro_moe_layer *page, const uint16_
 /* MlxRuntime::add of the two partial sparse outputs (paged_execution.rs:189-191):
  * out = bf16(float(a) + float(b)), round to nearest even. */
 int astro_moe_add(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, void *stream);
+
+/*
+ * ------------------------------------------------------------------ expert pages from safetensors
+ * Host-side I/O; no kernel runs.  The checkpoint keeps each projection of a layer as three
+ * rank-3 tensors "<layer_prefix>.switch_mlp.<proj>.<param>" (proj: gate_proj, up_proj,
+ * down_proj; param: weight (U32 codes), scales, biases), each [experts, out, inner] and
+ * possibly in different shard files.  The loader reads exactly the byte intervals of the
+ * selected experts (never a whole shard) and writes them, unchanged, into the caller's
+ * buffers in the MLX affine layout the block reads.
+ */
+enum astro_moe_dtype {  /* the safetensors dtypes MLX 0.32 reads (safetensors_header.rs:23-38) */
+  ASTRO_MOE_DTYPE_BOOL = 0, ASTRO_MOE_DTYPE_I8, ASTRO_MOE_DTYPE_U8, ASTRO_MOE_DTYPE_F8_E4M3,
+  ASTRO_MOE_DTYPE_F8_E5M2, ASTRO_MOE_DTYPE_I16, ASTRO_MOE_DTYPE_U16, ASTRO_MOE_DTYPE_F16,
+  ASTRO_MOE_DTYPE_BF16, ASTRO_MOE_DTYPE_I32, ASTRO_MOE_DTYPE_U32, ASTRO_MOE_DTYPE_F32,
+  ASTRO_MOE_DTYPE_I64, ASTRO_MOE_DTYPE_U64
+};
+
+#define ASTRO_MOE_PATH_MAX 1024
+
+/* One full expert tensor of a layer: quantized_expert_manifest.rs:300-315 (QuantizedTensorSource). */
+typedef struct astro_moe_tensor_source {
+  char source_file[ASTRO_MOE_PATH_MAX];  /* shard path */
+  int32_t dtype;                         /* astro_moe_dtype */
+  int64_t shape[3];                      /* [expert capacity, out, inner] */
+  uint64_t file_offset;                  /* file-relative offset of expert 0 */
+  uint64_t bytes_per_expert;
+  uint64_t file_size;
+} astro_moe_tensor_source;
+
+/* Startup-validated layer plan: quantized_expert_manifest.rs:317-326 plus the resident gate/up
+ * fusion decision (resident_gate_up_fusion.rs:109-163). */
+typedef struct astro_moe_expert_layer_plan {
+  astro_moe_tensor_source src[3][3];  /* [gate_proj, up_proj, down_proj][weight, scales, biases] */
+  int32_t expert_capacity;
+  int32_t bits[3], group_size[3];     /* per projection */
+  int32_t gate_up_fusable;            /* 1: gate and up may be concatenated on the output axis */
+  char gate_up_separate_reason[96];   /* why not, when gate_up_fusable == 0 */
+} astro_moe_expert_layer_plan;
+
+/* One read of a selected-expert run: source_manifests.rs:46-58 (QuantizedExpertSourceInterval).
+ * virtual_offset is the run's offset inside its tensor's compact page payload. */
+typedef struct astro_moe_page_interval {
+  int32_t projection, parameter;      /* src indices */
+  int32_t expert_start, expert_count, first_page_slot;
+  uint64_t file_offset, byte_count, virtual_offset;
+} astro_moe_page_interval;
+
+/* Parses the safetensors framing of `path` (8-byte little-endian length, JSON header of at most
+ * 64 MiB) with every check of parse_safetensors_header (safetensors_header.rs:171-276), then
+ * looks up one tensor.  shape holds up to 8 dimensions; file_offset is file-relative. */
+int astro_moe_safetensors_tensor(const char *path, const char *tensor_name, int32_t *dtype,
+                                 int32_t *rank, int64_t *shape, uint64_t *file_offset,
+                                 uint64_t *byte_count);
+
+/* build_quantized_expert_layer_plan (quantized_expert_layer_plan.rs:29-214): weight_map pairs
+ * tensor names with shard file names relative to model_dir (model.safetensors.index.json);
+ * bits / group_size are the quantization profile of each projection. */
+int astro_moe_build_expert_layer_plan(const char *model_dir, const char *const *map_tensor_names,
+                                      const char *const *map_shard_files, int32_t map_len,
+                                      const char *layer_prefix, const int32_t bits[3],
+                                      const int32_t group_size[3], astro_moe_expert_layer_plan *plan);
+
+/* build_quantized_expert_page_manifest_from_plan (quantized_expert_manifest.rs:401-418):
+ * validates expert_ids (non-empty, strictly ascending, below the capacity), fills
+ * slot_of_expert[capacity] (0xffffffff where absent) and, when intervals is non-null, the
+ * reads of every tensor's contiguous selected runs (9 * n at most); payload_bytes = compact
+ * page bytes over all 9 tensors. */
+int astro_moe_build_expert_page_manifest(const astro_moe_expert_layer_plan *plan,
+                                         const int32_t *expert_ids, int32_t n, uint32_t *slot_of_expert,
+                                         astro_moe_page_interval *intervals, int32_t max_intervals,
+                                         int32_t *n_intervals, uint64_t *payload_bytes);
+
+/* load_quantized_expert_page (bounded_expert_reader.rs:35-117) and, with fuse_gate_up, the
+ * resident concatenation of gate and up on the output axis (resident_gate_up_fusion.rs:221-260).
+ * dst[p][q] receives tensor src[p][q] of the selected experts, [n, out, inner] in page-slot
+ * order; with fuse_gate_up (requires plan->gate_up_fusable) dst[0][q] receives
+ * [n, 2 * out, inner] = each expert's gate rows then its up rows and dst[1][*] is unused.
+ * dst_on_device: destinations are HIP device memory, written through `staging` (pinned host
+ * memory of staging_bytes >= 1 MiB; null: the call allocates and frees its own) on `stream`,
+ * which is synchronized before returning; otherwise host memory.  bytes_read = file bytes read. */
+int astro_moe_load_expert_page(const astro_moe_expert_layer_plan *plan, const int32_t *expert_ids,
+                               int32_t n, int32_t fuse_gate_up, void *const *dst, int32_t dst_on_device,
+                               void *staging, size_t staging_bytes, void *stream, uint64_t *bytes_read);
 
 /*
  * Seeded synthetic inputs for benchmarks and tests (no counterpart in the reference):
