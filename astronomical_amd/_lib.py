@@ -71,6 +71,14 @@ class PageInterval(C.Structure):
 
 
 EXPORTS = {
+    "astro_moe_add_rms_norm": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_float, C.c_int32, C.c_int32,
+                                C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_decoder_ffn_workspace_bytes": ([C.POINTER(Layer), C.c_int32, C.POINTER(C.c_size_t)], C.c_int),
+    "astro_moe_decoder_ffn_forward": ([C.POINTER(Layer), C.c_void_p, C.c_void_p, C.c_void_p, C.c_float,
+                                       C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                       C.c_void_p], C.c_int),
+    "astro_moe_route_laguna": ([C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_double,
+                                C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "astro_moe_safetensors_tensor": ([C.c_char_p, C.c_char_p, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                       C.POINTER(C.c_int64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)],
                                      C.c_int),

@@ -988,4 +988,83 @@ int astro_moe_add(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out
   return e == hipSuccess ? ok() : hip_fail(op, e);
 }
 
+// ------------------------------------------------------------------ the decoder step around the block
+
+int astro_moe_add_rms_norm(const uint16_t *hidden, const uint16_t *attention_out, const uint16_t *norm_weight,
+                           float eps, int32_t tokens, int32_t hidden_size, uint16_t *residual_out,
+                           uint16_t *normed_out, void *stream) {
+  const char *op = "apply MLX RMS normalization";  // mlx_operations.rs:97
+  if (tokens < 0 || hidden_size <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "token count must not be negative and the hidden size positive");
+  if (hidden_size > 8192) return fail(ASTRO_MOE_UNSUPPORTED, op, "the normalization kernel supports hidden sizes up to 8192");
+  if (!(eps >= 0.0f)) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "epsilon must be a non-negative number");
+  if (tokens == 0) return ok();
+  if (!hidden || !norm_weight || !normed_out)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "hidden states, weight and output must be non-null");
+  hipError_t e = launch_add_rms_norm(hidden, attention_out, norm_weight, eps, tokens, hidden_size,
+                                     residual_out, normed_out, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(op, e);
+}
+
+static size_t ffn_extra_bytes(int T, int H) { return 3 * align_up((size_t)T * H * 2); }
+
+int astro_moe_decoder_ffn_workspace_bytes(const astro_moe_layer *layer, int32_t tokens, size_t *bytes) {
+  size_t blk = 0;
+  int rc = astro_moe_workspace_bytes(layer, tokens, &blk);
+  if (rc) return rc;
+  *bytes = align_up(blk) + ffn_extra_bytes(tokens, layer->hidden);
+  return ok();
+}
+
+int astro_moe_decoder_ffn_forward(const astro_moe_layer *layer, const uint16_t *hidden,
+                                  const uint16_t *attention_out, const uint16_t *norm_weight, float eps,
+                                  int32_t tokens, uint16_t *out, uint16_t *residual_out, void *workspace,
+                                  size_t workspace_bytes, void *stream) {
+  const char *op = "run the Qwen3.5 decoder feed-forward step";
+  size_t blk = 0;
+  int rc = astro_moe_workspace_bytes(layer, tokens, &blk);
+  if (rc) return rc;
+  const int H = layer->hidden;
+  const size_t need = align_up(blk) + ffn_extra_bytes(tokens, H);
+  if (!workspace || workspace_bytes < need) return workspace_fail(op, need, workspace ? workspace_bytes : 0);
+  if (tokens == 0) return ok();
+  if (!hidden || !norm_weight || !out) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "hidden states, weight and output must be non-null");
+  if (!(eps >= 0.0f)) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "epsilon must be a non-negative number");
+  if (H > 8192) return fail(ASTRO_MOE_UNSUPPORTED, op, "the normalization kernel supports hidden sizes up to 8192");
+  char *ws = (char *)workspace;
+  uint16_t *r = (uint16_t *)(ws + align_up(blk));
+  uint16_t *n = (uint16_t *)((char *)r + align_up((size_t)tokens * H * 2));
+  uint16_t *y = (uint16_t *)((char *)n + align_up((size_t)tokens * H * 2));
+  if (residual_out) r = residual_out;
+  hipStream_t s = (hipStream_t)stream;
+  // attention_residual, normalized_attention (decoder_layer_forward.rs:111-116)
+  hipError_t e = launch_add_rms_norm(hidden, attention_out, norm_weight, eps, tokens, H, r, n, s);
+  if (e != hipSuccess) return hip_fail(op, e);
+  rc = astro_moe_block_forward(layer, n, tokens, y, workspace, blk, stream);
+  if (rc) return rc;
+  // attention_residual + mlp_output (decoder_layer_forward.rs:171-173)
+  e = launch_add_bf16(r, y, (int64_t)tokens * H, out, s);
+  return e == hipSuccess ? ok() : hip_fail(op, e);
+}
+
+// route_laguna_experts (laguna/moe/router.rs:29-94) with the CPU selection order
+int astro_moe_route_laguna(const uint16_t *logits, int32_t tokens, int32_t experts, int32_t top_k,
+                           const float *correction_bias, double softcap, int32_t normalize,
+                           uint32_t *indices, float *scores, void *stream) {
+  const char *op = "route Laguna sparse experts";
+  if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "router logits must include token and expert dimensions");
+  if (experts <= 0 || top_k <= 0 || top_k > experts)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op,
+                "selected expert count must be positive and no larger than the router dimension");
+  if (!(softcap >= 0.0))  // router_selection.rs:125-139
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "Laguna router logits, top-K, and softcap must describe a valid selection");
+  if (experts > 1024 || top_k > 64)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "the router kernel supports at most 1024 experts and top-64");
+  if (tokens == 0) return ok();
+  if (!logits || !indices || !scores) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "router buffers must be non-null");
+  hipError_t e = launch_route_laguna(logits, tokens, experts, top_k, correction_bias, (float)softcap, normalize,
+                                     indices, scores, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(op, e);
+}
+
 }  // extern "C"

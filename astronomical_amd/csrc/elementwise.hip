@@ -244,7 +244,157 @@ __global__ __launch_bounds__(256) void add_bf16_kernel(const uint16_t *__restric
   if (i < n) out[i] = (uint16_t)f2bf(bf2f(a[i]) + bf2f(b[i]));
 }
 
+// The decoder's RMSNorm input of the block (decoder_layer_forward.rs:111-116 with MLX
+// fast::rms_norm): r = bf16(h + a) (a may be null: r = h), n = bf16(w * bf16(r * inv)) with
+// inv = 1 / sqrt(mean(r^2) + eps) in fp32 (IEEE sqrt and division).  mean(r^2) in a fixed
+// order the host oracle repeats: thread j of the 256 sums r_i^2 for i = j, j + 256, ... in
+// turn, each wave combines its lanes by the canonical butterfly (wave_sum) and the four wave
+// sums add as (w0 + w1) + (w2 + w3).  One workgroup per token row.
+template <int PER>
+__global__ __launch_bounds__(256) void add_rms_norm_kernel(const uint16_t *__restrict__ h,
+                                                           const uint16_t *__restrict__ a,
+                                                           const uint16_t *__restrict__ w, float eps,
+                                                           int H, uint16_t *__restrict__ r_out,
+                                                           uint16_t *__restrict__ n_out) {
+#pragma clang fp contract(off)
+  __shared__ float wsum[4];
+  const int64_t row = (int64_t)blockIdx.x * H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  float rv[PER];
+  float part = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = tid + 256 * i;
+    float v = 0.0f;
+    if (e < H) {
+      v = bf2f(h[row + e]);
+      if (a) v = round_bf(v + bf2f(a[row + e]));
+      if (r_out) r_out[row + e] = (uint16_t)f2bf(v);
+    }
+    rv[i] = v;
+    part = part + v * v;
+  }
+  const float ws = wave_sum(part);
+  if (lane == 0) wsum[wave] = ws;
+  __syncthreads();
+  const float total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = tid + 256 * i;
+    if (e < H) n_out[row + e] = (uint16_t)f2bf(bf2f(w[e]) * round_bf(rv[i] * inv));
+  }
+}
+
+// tanh(x) = sign(x) (1 - 2 / (e^(2|x|) + 1)) on det_expf: the same steps on the host give the
+// same bits
+__device__ __forceinline__ float det_tanh(float x) {
+#pragma clang fp contract(off)
+  const float ax = __builtin_fabsf(x);
+  const float t = 1.0f - 2.0f / (det_expf(2.0f * ax) + 1.0f);
+  return x != x ? x : __builtin_copysignf(t, x);
+}
+
+// route_laguna_experts (laguna/moe/router.rs:29-94) in the order of the reference's CPU
+// selection select_laguna_router_experts (router_selection.rs:59-116): one wave per token;
+// expert e scores s = sigmoid(l) of its fp32 logit l (after l = tanh(l / c) c when the softcap
+// c > 0); the k experts of largest s + bias (f32 total order, ties to the lower expert id) in
+// that descending order; their unbiased s, divided by the in-order fp32 sum of the k when
+// normalize and that sum is positive.  Keys: (total-order bits of s + bias) << 32 | ~e.
+template <int PER>
+__global__ __launch_bounds__(256) void laguna_route_kernel(const uint16_t *__restrict__ logits, int T,
+                                                           int E, int k, const float *__restrict__ bias,
+                                                           float softcap, int normalize,
+                                                           uint32_t *__restrict__ idx,
+                                                           float *__restrict__ scores) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  const uint16_t *l = logits + (int64_t)t * E;
+  auto score = [&](int e) {
+    float v = bf2f(l[e]);
+    if (softcap > 0.0f) v = det_tanh(v / softcap) * softcap;
+    return det_sigmoid(v);
+  };
+  uint64_t cand[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    const int ec = e < E ? e : E - 1;
+    const float sel = score(ec) + (bias ? bias[ec] : 0.0f);
+    uint32_t b = __float_as_uint(sel);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    cand[i] = e < E ? ((uint64_t)b << 32) | (uint64_t)(0xffffffffu - (uint32_t)e) : 0ull;
+  }
+  // per-lane descending order (odd-even transposition network)
+#pragma unroll
+  for (int pass = 0; pass < PER; ++pass)
+#pragma unroll
+    for (int i = pass & 1; i + 1 < PER; i += 2) {
+      const uint64_t hi = cand[i] > cand[i + 1] ? cand[i] : cand[i + 1];
+      const uint64_t lo = cand[i] > cand[i + 1] ? cand[i + 1] : cand[i];
+      cand[i] = hi;
+      cand[i + 1] = lo;
+    }
+  uint64_t mine = 0;
+  for (int r = 0; r < k; ++r) {
+    uint64_t top = cand[0];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)top, off, kWave);
+      const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(top >> 32), off, kWave);
+      const uint64_t o = ((uint64_t)hi << 32) | lo;
+      top = o > top ? o : top;
+    }
+    const bool hit = cand[0] == top;
+#pragma unroll
+    for (int i = 0; i + 1 < PER; ++i) cand[i] = hit ? cand[i + 1] : cand[i];
+    cand[PER - 1] = hit ? 0ull : cand[PER - 1];
+    mine = lane == r ? top : mine;
+  }
+  const uint32_t e = 0xffffffffu - (uint32_t)mine;
+  float s = lane < k ? score(e) : 0.0f;
+  if (normalize) {
+    float sum = 0.0f;
+    for (int j = 0; j < k; ++j) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), j));
+    if (sum > 0.0f) s = s / sum;
+  }
+  if (lane < k) {
+    idx[(int64_t)t * k + lane] = e;
+    scores[(int64_t)t * k + lane] = s;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_add_rms_norm(const uint16_t *h, const uint16_t *a, const uint16_t *w, float eps, int T,
+                               int H, uint16_t *r_out, uint16_t *n_out, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  const int per = (H + 255) / 256;
+#define ASTRO_RMS(P) hipLaunchKernelGGL(add_rms_norm_kernel<P>, dim3(T), dim3(256), 0, s, h, a, w, eps, H, r_out, n_out)
+  if (per <= 4) ASTRO_RMS(4);
+  else if (per <= 8) ASTRO_RMS(8);
+  else if (per <= 16) ASTRO_RMS(16);
+  else ASTRO_RMS(32);
+#undef ASTRO_RMS
+  return hipGetLastError();
+}
+
+hipError_t launch_route_laguna(const uint16_t *logits, int T, int E, int k, const float *bias, float softcap,
+                               int normalize, uint32_t *idx, float *scores, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  const int per = (E + 63) / 64;
+  const dim3 grid((T + 3) / 4), block(256);
+#define ASTRO_LAG(P) hipLaunchKernelGGL(laguna_route_kernel<P>, grid, block, 0, s, logits, T, E, k, bias, softcap, normalize, idx, scores)
+  if (per <= 1) ASTRO_LAG(1);
+  else if (per <= 2) ASTRO_LAG(2);
+  else if (per <= 4) ASTRO_LAG(4);
+  else if (per <= 8) ASTRO_LAG(8);
+  else ASTRO_LAG(16);
+#undef ASTRO_LAG
+  return hipGetLastError();
+}
 
 hipError_t launch_remap_slots(const uint32_t *ids, int n, const uint32_t *slot_of_expert, int experts,
                               uint32_t *slots, uint32_t *missing, hipStream_t s) {

@@ -84,6 +84,13 @@ hipError_t launch_gather_assignments(const uint32_t *ids, const uint16_t *scores
                                      uint16_t *out_scores, hipStream_t s);
 hipError_t launch_add_bf16(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t *p, int n, hipStream_t s);  // a kernel, safe in graph capture
+// decoder step around the block: r = bf16(h + a) (a nullable; r_out nullable), n = RMSNorm(r)
+// with weight w (H <= 8192)
+hipError_t launch_add_rms_norm(const uint16_t *h, const uint16_t *a, const uint16_t *w, float eps, int T,
+                               int H, uint16_t *r_out, uint16_t *n_out, hipStream_t s);
+// Laguna's sigmoid router (E <= 1024, k <= 64): idx u32 [T][k], fp32 scores [T][k]
+hipError_t launch_route_laguna(const uint16_t *logits, int T, int E, int k, const float *bias, float softcap,
+                               int normalize, uint32_t *idx, float *scores, hipStream_t s);
 // y = weighted sum of expert rows (rows located through inverse_order), sorted (fp32
 // fma accumulation) or unsorted (bf16 products) rounding, then optionally the shared
 // expert's gated add.

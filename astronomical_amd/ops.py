@@ -321,6 +321,27 @@ class MoeBlock:
 
     __call__ = forward
 
+    def decoder_feed_forward(self, hidden: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                             attention_out: Optional[torch.Tensor] = None,
+                             out: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+                             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The feed-forward half of a decoder layer around this block
+        (decoder_layer_forward.rs:111-174): r = hidden + attention_out, n = rms_norm(r),
+        out = r + MoE(n), all bf16; `residual` (optional) receives r."""
+        h2 = hidden.contiguous().view(torch.bfloat16).reshape(-1, self.weights.hidden)
+        T = h2.shape[0]
+        a2 = None if attention_out is None else attention_out.contiguous().view(torch.bfloat16).reshape(T, -1)
+        y = out if out is not None else torch.empty_like(h2)
+        n = C.c_size_t()
+        call("astro_moe_decoder_ffn_workspace_bytes", C.byref(self._struct), T, C.byref(n))
+        ws = workspace
+        if ws is None or ws.numel() < n.value:
+            ws = torch.empty(max(n.value, 1), dtype=torch.uint8, device=self.device)
+        w = norm_weight.contiguous().view(torch.bfloat16)
+        call("astro_moe_decoder_ffn_forward", C.byref(self._struct), _ptr(h2), _ptr(a2), _ptr(w), float(eps), T,
+             _ptr(y), _ptr(residual), _ptr(ws), ws.numel(), _stream(self.device))
+        return y
+
     def forward_attributed(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
                            workspace: Optional[torch.Tensor] = None):
         """forward plus per-stage device milliseconds (synchronises the stream)."""
@@ -436,6 +457,37 @@ def forward_moe_with_streamed_weights(hidden_states: torch.Tensor, page: MoeLaye
     call("astro_moe_streamed_sparse_forward", C.byref(s), _ptr(x2), T, _ptr(slots), _ptr(sc), kk,
          _ptr(out), _ptr(ws), need.value, _stream(x2.device))
     return out
+
+
+def rms_norm(hidden: torch.Tensor, weight: torch.Tensor, eps: float,
+             attention_out: Optional[torch.Tensor] = None, residual_out: Optional[torch.Tensor] = None
+             ) -> torch.Tensor:
+    """MlxRuntime::rms_norm (mlx_operations.rs:91-101) of hidden (+ attention_out, the decoder's
+    attention residual, written to residual_out when given), bf16 [..., H]."""
+    H = hidden.shape[-1]
+    h2 = hidden.contiguous().view(torch.bfloat16).reshape(-1, H)
+    a2 = None if attention_out is None else attention_out.contiguous().view(torch.bfloat16).reshape(-1, H)
+    out = torch.empty_like(h2)
+    call("astro_moe_add_rms_norm", _ptr(h2), _ptr(a2), _ptr(weight.contiguous().view(torch.bfloat16)), float(eps),
+         h2.shape[0], H, _ptr(residual_out), _ptr(out), _stream(h2.device))
+    return out.reshape(hidden.shape)
+
+
+def route_laguna_experts(router_logits: torch.Tensor, experts_per_token: int,
+                         correction_bias: Optional[torch.Tensor] = None, router_logit_softcap: float = 0.0,
+                         normalize: bool = True):
+    """route_laguna_experts (laguna/moe/router.rs:29-94): (selected indices int32 [..., k],
+    fp32 scores [..., k]) in the order of the CPU selection (router_selection.rs:59-116)."""
+    lg = router_logits.contiguous().view(torch.bfloat16)
+    E = lg.shape[-1]
+    T = lg.numel() // max(E, 1)
+    shape = tuple(lg.shape[:-1]) + (experts_per_token,)
+    idx = torch.empty(shape, dtype=torch.int32, device=lg.device)
+    sc = torch.empty(shape, dtype=torch.float32, device=lg.device)
+    bias = None if correction_bias is None else correction_bias.contiguous().to(torch.float32)
+    call("astro_moe_route_laguna", _ptr(lg), T, E, experts_per_token, _ptr(bias), float(router_logit_softcap),
+         int(normalize), _ptr(idx), _ptr(sc), _stream(lg.device))
+    return idx, sc
 
 
 def add(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

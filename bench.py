@@ -196,7 +196,10 @@ def main():
     log(f"prefill: {prefill_ms * 1000:.1f} us")
 
     # ---------------------------------------------------------------- side measurements
-    extra = None if args.no_extra else other_configs(CF, DS, ops, torch, K, W, layers[0])
+    extra = None
+    if not args.no_extra:
+        extra = decoder_step(CF, DS, ops, torch, blocks, K, W)
+        extra.update(other_configs(CF, DS, ops, torch, K, W, layers[0]))
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
@@ -330,6 +333,70 @@ def other_configs(CF, DS, ops, torch, K, W, layer_c1):
     torch.cuda.empty_cache()
     log(f"other configs: {json.dumps(out)}")
     return out
+
+
+def decoder_step(CF, DS, ops, torch, blocks, K, W):
+    """The decoder's feed-forward step around the block (residual add + RMS norm, block,
+    residual add) on the c1 layers: decode B=1 through a graph of all the layers, 2048-token
+    prefill on layer 0, the RMS norm kernel alone, and Laguna's sigmoid router on c2-sized
+    logits."""
+    cfg = CF.C1
+    H, nL, dev = cfg.hidden, len(blocks), torch.device("cuda")
+    w = DS.make_tokens_device(cfg, 1, step=7).reshape(H)  # a bf16 weight vector (values ~N(0,1))
+    T2 = 2048
+    ws = torch.empty(blocks[0].workspace_bytes(T2) + 3 * T2 * H * 2 + 1024, dtype=torch.uint8, device=dev)
+    h = DS.make_tokens_device(cfg, nL, step=3).reshape(nL, 1, H)
+    a = DS.make_tokens_device(cfg, nL, step=4).reshape(nL, 1, H)
+    outs = torch.empty_like(h)
+
+    def step():
+        for l in range(nL):
+            blocks[l].decoder_feed_forward(h[l], w, 1e-6, attention_out=a[l], out=outs[l], workspace=ws)
+    step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(W):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(K):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    dec_us = e0.elapsed_time(e1) / K / nL * 1000
+
+    def timed(fn, iters=10):
+        fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(iters):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / iters * 1000
+
+    xp = DS.make_tokens_device(CF.C2, T2)
+    ap = DS.make_tokens_device(CF.C2, T2, step=5)
+    yp = torch.empty_like(xp)
+    rp = torch.empty_like(xp)
+    pre_us = timed(lambda: blocks[0].decoder_feed_forward(xp, w, 1e-6, attention_out=ap, out=yp, workspace=ws))
+    rms_us = timed(lambda: ops.rms_norm(xp, w, 1e-6, attention_out=ap, residual_out=rp), 20)
+    rms_bytes = 4 * T2 * H * 2  # read h and a, write r and n
+    logits = DS.make_tokens_device(CF.C2, T2, step=6)[:, :cfg.experts].contiguous()
+    bias = torch.zeros(cfg.experts, dtype=torch.float32, device=dev)
+    lag_us = timed(lambda: ops.route_laguna_experts(logits, cfg.top_k, bias, 0.0, True), 20)
+    return {"decoder_ffn_step": {
+        "workload": f"c1 residual add + RMS norm + MoE block + residual add: decode B=1 through a graph of {nL} "
+                    f"layers, and {T2}-token prefill on one layer",
+        "decode_us_per_layer": round(dec_us, 2), "decode_tokens_per_s": round(1e6 / dec_us, 1),
+        "prefill_us": round(pre_us, 1),
+        "rms_norm_us_2048": round(rms_us, 2), "rms_norm_GBps": round(rms_bytes / (rms_us * 1e-6) / 1e9, 1)},
+        "laguna_route": {"workload": f"Laguna sigmoid router, {T2} tokens x {cfg.experts} experts, top-{cfg.top_k}, "
+                                     "correction bias, normalised", "us": round(lag_us, 2)}}
 
 
 def page_load(CF, torch, L, n_experts=16, ids=(1, 3, 4, 6, 8, 10, 12, 15), reps=5):

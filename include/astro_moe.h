@@ -271,6 +271,39 @@ int astro_moe_streamed_sparse_forward(const astro_moe_layer *page, const uint16_
 int astro_moe_add(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, void *stream);
 
 /*
+ * ------------------------------------------------------------------ the decoder step around the block
+ * The feed-forward half of a Qwen3.5 decoder layer (forward_decoder_layer_attention's tail and
+ * forward_decoder_layer_feed_forward, decoder_layer_forward.rs:111-174):
+ *   r = bf16(hidden + attention_out)                    (attention_residual; attention_out NULL: r = hidden)
+ *   n = bf16(w * bf16(r * rsqrt(mean(r^2) + eps)))      (mlx_fast_rms_norm, fp32 inside)
+ *   out = bf16(r + MoE(n))
+ * All bf16 [tokens][hidden]; w bf16 [hidden]; hidden <= 8192.
+ */
+int astro_moe_add_rms_norm(const uint16_t *hidden, const uint16_t *attention_out, const uint16_t *norm_weight,
+                           float eps, int32_t tokens, int32_t hidden_size, uint16_t *residual_out,
+                           uint16_t *normed_out, void *stream);
+int astro_moe_decoder_ffn_workspace_bytes(const astro_moe_layer *layer, int32_t tokens, size_t *bytes);
+/* residual_out (nullable) receives r. */
+int astro_moe_decoder_ffn_forward(const astro_moe_layer *layer, const uint16_t *hidden,
+                                  const uint16_t *attention_out, const uint16_t *norm_weight, float eps,
+                                  int32_t tokens, uint16_t *out, uint16_t *residual_out, void *workspace,
+                                  size_t workspace_bytes, void *stream);
+
+/*
+ * Laguna's sigmoid router, the second router family over the same sparse experts:
+ * route_laguna_experts (laguna/moe/router.rs:29-94), emitted in the order of the reference's
+ * CPU selection select_laguna_router_experts (router_selection.rs:59-116).  Per token: fp32
+ * logit l (tanh-softcapped, l = tanh(l / softcap) * softcap, when softcap > 0), score
+ * s = sigmoid(l); the top_k experts of largest s + correction_bias (f32 total order, ties to the
+ * lower expert id) in that descending order; scores = their unbiased s, divided by their
+ * in-order fp32 sum when normalize and the sum is positive.  logits bf16 [tokens][experts];
+ * correction_bias fp32 [experts] or NULL; indices u32 [tokens][top_k]; scores fp32 [tokens][top_k].
+ */
+int astro_moe_route_laguna(const uint16_t *logits, int32_t tokens, int32_t experts, int32_t top_k,
+                           const float *correction_bias, double softcap, int32_t normalize,
+                           uint32_t *indices, float *scores, void *stream);
+
+/*
  * ------------------------------------------------------------------ expert pages from safetensors
  * Host-side I/O; no kernel runs.  The checkpoint keeps each projection of a layer as three
  * rank-3 tensors "<layer_prefix>.switch_mlp.<proj>.<param>" (proj: gate_proj, up_proj,

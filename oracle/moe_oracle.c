@@ -31,6 +31,13 @@
  *   orc_combine_shared   KAT [12,20] (routing_and_combination.rs:12-68)
  *   orc_moe_block_forward  composition of the above; fp64 brute force of the whole
  *                        block on a tiny layer (within bf16 rounding)
+ *   orc_add_rms_norm     fp64 closed form (<= 1 bf16 ulp per rounding step), constant rows,
+ *                        unit RMS of the unweighted output, eps dominance;
+ *                        tests/test_oracle_decoder.py
+ *   orc_decoder_ffn_forward  composition (residual add, RMS norm, block, residual add)
+ *   orc_laguna_route     reference KATs laguna_hermetic/routing.rs:8-60 (bias selects only,
+ *                        ties to the lower id, softcap before sigmoid, normalisation) and
+ *                        direct_mlx/laguna/routing.rs:63-122 ([0, 1] with bias); fp64 brute force
  * Reference choices that only an MLX build could pin (MLX 0.32.1 is not vendored):
  * the in-slice order of argpartition, MLX's CPU exp/sum order inside softmax, and its
  * accumulation order in quantized matmul.  The choices made here are stated at each
@@ -602,4 +609,141 @@ done:
   free(sparse); free(sorted_order); free(inverse); free(sorted_ids); free(x_rows);
   free(offsets);
   return rc;
+}
+
+/*
+ * The decoder step around the block (decoder_layer_forward.rs:111-174; the RMS norm of
+ * mlx_fast_rms_norm, mlx_operations.rs:91-101): r = bf16(h + a) (a may be NULL: r = h);
+ * n = bf16(w * bf16(r * inv)), inv = 1 / sqrt(mean(r^2) + eps) in fp32, IEEE sqrt and
+ * division.  MLX computes the normaliser in fp32, rounds x * inv to the input dtype and
+ * multiplies by the weight in that dtype (its fast::rms_norm fallback); the order of the
+ * fp32 sum of squares inside MLX is not pinned.  This restatement fixes it: partial j of 256
+ * sums r_i^2 for i = j, j + 256, ... in turn; the partials of each group of 64 combine by the
+ * butterfly of the softmax denominator, and the four group sums as (g0 + g1) + (g2 + g3).
+ */
+static void rms_norm_row(const float *r, const uint16_t *w, float eps, int32_t H, uint16_t *n) {
+  float part[256];
+  for (int j = 0; j < 256; ++j) {
+    float p = 0.0f;
+    for (int32_t i = j; i < H; i += 256) p = p + r[i] * r[i];
+    part[j] = p;
+  }
+  float g[4];
+  for (int q = 0; q < 4; ++q) {
+    float lane[ORC_LANES];
+    for (int j = 0; j < ORC_LANES; ++j) lane[j] = part[q * ORC_LANES + j];
+    for (int off = 1; off < ORC_LANES; off <<= 1) {
+      float next[ORC_LANES];
+      for (int j = 0; j < ORC_LANES; ++j) next[j] = lane[j] + lane[j ^ off];
+      for (int j = 0; j < ORC_LANES; ++j) lane[j] = next[j];
+    }
+    g[q] = lane[0];
+  }
+  const float total = (g[0] + g[1]) + (g[2] + g[3]);
+  const float inv = 1.0f / sqrtf(total / (float)H + eps);
+  for (int32_t i = 0; i < H; ++i) n[i] = tobf(bf(w[i]) * bf(tobf(r[i] * inv)));
+}
+
+int orc_add_rms_norm(const uint16_t *h, const uint16_t *a, const uint16_t *w, float eps, int32_t T,
+                     int32_t H, uint16_t *r_out, uint16_t *n_out) {
+  if (T < 0 || H <= 0) return ORC_ERR_GEOMETRY;
+  int err = ORC_OK;
+#pragma omp parallel num_threads(g_threads)
+  {
+    float *r = (float *)malloc(sizeof(float) * (size_t)H);
+    if (!r) {
+#pragma omp atomic write
+      err = ORC_ERR_GEOMETRY;
+    } else {
+#pragma omp for schedule(static)
+      for (int32_t t = 0; t < T; ++t) {
+        const size_t o = (size_t)t * H;
+        for (int32_t i = 0; i < H; ++i) {
+          float v = bf(h[o + i]);
+          if (a) v = bf(tobf(v + bf(a[o + i])));
+          r[i] = v;
+          if (r_out) r_out[o + i] = tobf(v);
+        }
+        rms_norm_row(r, w, eps, H, n_out + o);
+      }
+    }
+    free(r);
+  }
+  return err;
+}
+
+int orc_decoder_ffn_forward(const orc_layer *L, const uint16_t *h, const uint16_t *a, const uint16_t *w,
+                            float eps, int32_t T, uint16_t *out, uint16_t *r_out) {
+  const int32_t H = L->hidden;
+  uint16_t *r = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * H + 2);
+  uint16_t *n = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * H + 2);
+  uint16_t *y = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * H + 2);
+  int rc = (r && n && y) ? ORC_OK : ORC_ERR_GEOMETRY;
+  if (!rc) rc = orc_add_rms_norm(h, a, w, eps, T, H, r, n);
+  if (!rc) rc = orc_moe_block_forward(L, n, T, NULL, y, NULL);
+  if (!rc) {
+    for (size_t i = 0; i < (size_t)T * H; ++i) out[i] = tobf(bf(r[i]) + bf(y[i]));
+    if (r_out) memcpy(r_out, r, sizeof(uint16_t) * (size_t)T * H);
+  }
+  free(r);
+  free(n);
+  free(y);
+  return rc;
+}
+
+/*
+ * Laguna's sigmoid router: select_laguna_router_experts (laguna/moe/router_selection.rs:59-116),
+ * the reference's own CPU restatement of route_laguna_experts (laguna/moe/router.rs:29-94).
+ * Per token: l = fp32 logit, l = tanh(l / c) * c when the softcap c > 0, s = sigmoid(l),
+ * selection key s + bias; experts sorted by key descending (f32 total order) with the lower
+ * expert id first on ties; the first k in that order; their unbiased s, divided by the
+ * in-order fp32 sum when normalize and the sum is positive.  exp is orc_expf (the device's
+ * det_expf bit for bit); tanh(x) = sign(x) (1 - 2 / (e^(2|x|) + 1)) on it.
+ */
+static float tanh_det(float x) {
+  const float t = 1.0f - 2.0f / (orc_expf(2.0f * fabsf(x)) + 1.0f);
+  return x != x ? x : copysignf(t, x);
+}
+
+static uint32_t total_order_bits(float f) {
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+int orc_laguna_route(const uint16_t *logits, int32_t T, int32_t E, int32_t k, const float *bias,
+                     float softcap, int32_t normalize, uint32_t *indices, float *scores) {
+  if (T < 0 || E <= 0 || k <= 0 || k > E || !(softcap >= 0.0f)) return ORC_ERR_GEOMETRY;
+  uint64_t *keys = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)E);
+  float *s = (float *)malloc(sizeof(float) * (size_t)E);
+  if (!keys || !s) {
+    free(keys);
+    free(s);
+    return ORC_ERR_GEOMETRY;
+  }
+  for (int32_t t = 0; t < T; ++t) {
+    for (int32_t e = 0; e < E; ++e) {
+      float l = bf(logits[(size_t)t * E + e]);
+      if (softcap > 0.0f) l = tanh_det(l / softcap) * softcap;
+      s[e] = sigmoidf_det(l);
+      const float sel = s[e] + (bias ? bias[e] : 0.0f);
+      keys[e] = ((uint64_t)total_order_bits(sel) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
+    }
+    /* k selections of the largest remaining key: descending key = descending score, lower id first */
+    float sum = 0.0f;
+    for (int32_t j = 0; j < k; ++j) {
+      int32_t best = 0;
+      for (int32_t e = 1; e < E; ++e)
+        if (keys[e] > keys[best]) best = e;
+      indices[(size_t)t * k + j] = (uint32_t)best;
+      scores[(size_t)t * k + j] = s[best];
+      sum = sum + s[best];
+      keys[best] = 0;
+    }
+    if (normalize && sum > 0.0f)
+      for (int32_t j = 0; j < k; ++j) scores[(size_t)t * k + j] = scores[(size_t)t * k + j] / sum;
+  }
+  free(keys);
+  free(s);
+  return ORC_OK;
 }

@@ -115,11 +115,19 @@ void orc_unsorted_weighted_sum(const uint16_t *out, const uint16_t *scores, int3
 void orc_combine_shared(const uint16_t *sparse, const uint16_t *shared_out,
                         const uint16_t *gate_logits, int32_t T, int32_t D, uint16_t *y);
 
+/* the decoder step around the block and Laguna's sigmoid router */
+int orc_add_rms_norm(const uint16_t *h, const uint16_t *a, const uint16_t *w, float eps, int32_t T,
+                     int32_t H, uint16_t *r_out, uint16_t *n_out);
+int orc_laguna_route(const uint16_t *logits, int32_t T, int32_t E, int32_t k, const float *bias,
+                     float softcap, int32_t normalize, uint32_t *indices, float *scores);
+
 /* whole block; logits_override (bf16 [T][E], may be NULL) replaces the router
  * projection so routing can be compared on identical logits. */
 int orc_moe_block_forward(const orc_layer *L, const uint16_t *x, int32_t T,
                           const uint16_t *logits_override, uint16_t *y,
                           orc_trace *trace);
+int orc_decoder_ffn_forward(const orc_layer *L, const uint16_t *h, const uint16_t *a, const uint16_t *w,
+                            float eps, int32_t T, uint16_t *out, uint16_t *r_out);
 
 #ifdef __cplusplus
 }

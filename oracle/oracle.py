@@ -81,8 +81,12 @@ def lib():
         L.orc_unsorted_weighted_sum.argtypes = [vp, vp, i32, i32, i32, vp]
         L.orc_combine_shared.argtypes = [vp, vp, vp, i32, i32, vp]
         L.orc_moe_block_forward.argtypes = [C.POINTER(_Layer), vp, i32, vp, vp, C.POINTER(_Trace)]
+        L.orc_add_rms_norm.argtypes = [vp, vp, vp, C.c_float, i32, i32, vp, vp]
+        L.orc_laguna_route.argtypes = [vp, i32, i32, i32, vp, C.c_float, i32, vp, vp]
+        L.orc_decoder_ffn_forward.argtypes = [C.POINTER(_Layer), vp, vp, vp, C.c_float, i32, vp, vp]
         for f in ("orc_route_topk", "orc_sort_assignments", "orc_invert_assignment_order",
-                  "orc_dequantize", "orc_qmm", "orc_gather_qmm", "orc_moe_block_forward"):
+                  "orc_dequantize", "orc_qmm", "orc_gather_qmm", "orc_moe_block_forward",
+                  "orc_add_rms_norm", "orc_laguna_route", "orc_decoder_ffn_forward"):
             getattr(L, f).restype = C.c_int
         _lib = L
     return _lib
@@ -284,6 +288,47 @@ def moe_block_forward(L, x, logits_override=None, trace=False):
         bufs["used_sorted_path"] = bool(tr.used_sorted_path)
         return y, bufs
     return y
+
+
+# ------------------------------------------------------------------- the decoder step and Laguna's router
+
+def add_rms_norm(h, w, eps, a=None):
+    """(r, n): r = bf16(h + a) (h when a is None), n = RMS norm of r with weight w (bf16 [T, H])."""
+    h = _c(h, np.uint16)
+    T, H = h.shape
+    a = None if a is None else _c(a, np.uint16)
+    w = _c(w, np.uint16)
+    r = np.empty((T, H), np.uint16)
+    n = np.empty((T, H), np.uint16)
+    _check(lib().orc_add_rms_norm(_p(h), _p(a), _p(w), float(eps), T, H, _p(r), _p(n)), "add rms norm")
+    return r, n
+
+
+def decoder_ffn_forward(L, h, w, eps, a=None):
+    """(out, r): out = bf16(r + MoE(rms_norm(r))), r = bf16(h + a)."""
+    keep = []
+    s = layer_struct(L, keep)
+    h = _c(h, np.uint16)
+    T = h.shape[0]
+    a = None if a is None else _c(a, np.uint16)
+    w = _c(w, np.uint16)
+    out = np.empty_like(h)
+    r = np.empty_like(h)
+    _check(lib().orc_decoder_ffn_forward(C.byref(s), _p(h), _p(a), _p(w), float(eps), T, _p(out), _p(r)),
+           "decoder feed-forward step")
+    return out, r
+
+
+def laguna_route(logits, k, bias=None, softcap=0.0, normalize=True):
+    """(indices uint32 [T, k], fp32 scores [T, k]) of the CPU selection order."""
+    lg = _c(logits, np.uint16)
+    T, E = lg.shape
+    b = None if bias is None else _c(bias, np.float32)
+    idx = np.empty((T, k), np.uint32)
+    sc = np.empty((T, k), np.float32)
+    _check(lib().orc_laguna_route(_p(lg), T, E, k, _p(b), float(softcap), int(normalize), _p(idx), _p(sc)),
+           "laguna route")
+    return idx, sc
 
 
 # ------------------------------------------------------------------- paged callers
