@@ -449,8 +449,17 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
 }
 
 // The block's launch sequence; clock (nullable) collects per-stage times.
+// The decoder step around the block (astro_moe_decoder_ffn_forward): x must be n; the decode
+// kernels fuse r, n and out when the T rows fit their LDS, otherwise separate kernels run.
+struct DecoderStep {
+  const uint16_t *h, *a, *w;
+  float eps;
+  uint16_t *r, *n, *out;
+};
+
 int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, uint16_t *y,
-              void *workspace, size_t workspace_bytes, void *stream, StageClock *clock) {
+              void *workspace, size_t workspace_bytes, void *stream, StageClock *clock,
+              const DecoderStep *step = nullptr) {
   int rc = check_layer(kBlockOp, layer);
   if (rc) return rc;
   if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
@@ -487,6 +496,17 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   const bool has_shared = L.shared_intermediate > 0;
   uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
   uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
+  const bool fuse_step = step && o.decode && (size_t)T * H * 2 <= (size_t)kDecodeStepLds && H % 8 == 0;
+  if (step && !fuse_step) {
+    // attention_residual and normalized_attention (decoder_layer_forward.rs:111-116)
+    hipError_t e = launch_add_rms_norm(step->h, step->a, step->w, step->eps, T, H, step->r, step->n, s);
+    if (e != hipSuccess) return hip_fail(kBlockOp, e);
+  }
+  auto finish = [&]() {  // attention_residual + mlp_output (decoder_layer_forward.rs:171-173)
+    if (!step || fuse_step) return ok();
+    hipError_t e = launch_add_bf16(step->r, y, (int64_t)T * H, step->out, s);
+    return e == hipSuccess ? ok() : hip_fail(kBlockOp, e);
+  };
 
   if (o.decode) {
     DecodeArgs d{};
@@ -570,6 +590,15 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     d.router_blocks = (E + 3) / 4;
     d.shared_pair_blocks = has_shared ? (d.Is + 4 * kDecodeRowsPerWave - 1) / (4 * kDecodeRowsPerWave) : 0;
     d.max_groups = std::min(A, E);
+    if (fuse_step) {
+      d.h_in = step->h;
+      d.a_in = step->a;
+      d.norm_w = step->w;
+      d.eps = step->eps;
+      d.r_out = step->r;
+      d.x_out = step->n;
+      d.ffn_out = step->out;
+    }
     if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
     // kernel-attached events: router | gate/up (shared gate/up, routing, sort inside) |
     // down (shared down and the combine inside)
@@ -584,7 +613,7 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     }
     hipError_t e = launch_decode_block(d, s, clock ? kev : nullptr);
     if (e != hipSuccess) return hip_fail(kBlockOp, e);
-    return ok();
+    return finish();
   }
 
   begin(0);
@@ -605,7 +634,7 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
   e = run_sparse(L, x, T, k, ids, scores, o, ws, true, y, s, clock);
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
-  return ok();
+  return finish();
 }
 
 }  // namespace
@@ -996,7 +1025,8 @@ int astro_moe_add_rms_norm(const uint16_t *hidden, const uint16_t *attention_out
   const char *op = "apply MLX RMS normalization";  // mlx_operations.rs:97
   if (tokens < 0 || hidden_size <= 0)
     return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "token count must not be negative and the hidden size positive");
-  if (hidden_size > 8192) return fail(ASTRO_MOE_UNSUPPORTED, op, "the normalization kernel supports hidden sizes up to 8192");
+  if (hidden_size > 8192 || hidden_size % 8 != 0)
+    return fail(ASTRO_MOE_UNSUPPORTED, op, "the normalization kernel supports hidden sizes that are multiples of 8 up to 8192");
   if (!(eps >= 0.0f)) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "epsilon must be a non-negative number");
   if (tokens == 0) return ok();
   if (!hidden || !norm_weight || !normed_out)
@@ -1036,15 +1066,8 @@ int astro_moe_decoder_ffn_forward(const astro_moe_layer *layer, const uint16_t *
   uint16_t *n = (uint16_t *)((char *)r + align_up((size_t)tokens * H * 2));
   uint16_t *y = (uint16_t *)((char *)n + align_up((size_t)tokens * H * 2));
   if (residual_out) r = residual_out;
-  hipStream_t s = (hipStream_t)stream;
-  // attention_residual, normalized_attention (decoder_layer_forward.rs:111-116)
-  hipError_t e = launch_add_rms_norm(hidden, attention_out, norm_weight, eps, tokens, H, r, n, s);
-  if (e != hipSuccess) return hip_fail(op, e);
-  rc = astro_moe_block_forward(layer, n, tokens, y, workspace, blk, stream);
-  if (rc) return rc;
-  // attention_residual + mlp_output (decoder_layer_forward.rs:171-173)
-  e = launch_add_bf16(r, y, (int64_t)tokens * H, out, s);
-  return e == hipSuccess ? ok() : hip_fail(op, e);
+  const DecoderStep step{hidden, attention_out, norm_weight, eps, r, n, out};
+  return run_block(layer, n, tokens, y, workspace, blk, stream, nullptr, &step);
 }
 
 // route_laguna_experts (laguna/moe/router.rs:29-94) with the CPU selection order

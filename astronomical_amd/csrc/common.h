@@ -133,6 +133,54 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
+// ---- RMS norm pieces shared by the standalone kernel and the decode router kernel
+// r = bf16(h + a) of 8 elements (a null: r = h)
+__device__ __forceinline__ u32x4 rms_residual(const u32x4 &h, const u32x4 *a) {
+#pragma clang fp contract(off)
+  if (!a) return h;
+  const u32x4 av = *a;
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = f2bf(bf_lo(h[i]) + bf_lo(av[i])) | (f2bf(bf_hi(h[i]) + bf_hi(av[i])) << 16);
+  return r;
+}
+// part + r_0^2 + ... + r_7^2, in element order
+__device__ __forceinline__ float rms_partial(const u32x4 &r, float part) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = bf_lo(r[i]), hi = bf_hi(r[i]);
+    part = part + lo * lo;
+    part = part + hi * hi;
+  }
+  return part;
+}
+// the workgroup (256 threads) total: canonical butterfly per wave, then (w0 + w1) + (w2 + w3);
+// wsum: 4 floats of LDS; every thread returns the total
+__device__ __forceinline__ float rms_total(float part, float *wsum) {
+#pragma clang fp contract(off)
+  const float ws = wave_sum(part);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ws;
+  __syncthreads();
+  const float t = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+  __syncthreads();  // wsum may be reused
+  return t;
+}
+__device__ __forceinline__ float rms_inverse(float total, int H, float eps) {
+#pragma clang fp contract(off)
+  return 1.0f / __builtin_sqrtf(total / (float)H + eps);
+}
+// n = bf16(w * bf16(r * inv)) of 8 elements
+__device__ __forceinline__ u32x4 rms_apply(const u32x4 &r, const u32x4 &w, float inv) {
+#pragma clang fp contract(off)
+  u32x4 n;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    n[i] = f2bf(bf_lo(w[i]) * round_bf(bf_lo(r[i]) * inv)) | (f2bf(bf_hi(w[i]) * round_bf(bf_hi(r[i]) * inv)) << 16);
+  return n;
+}
+
 // DPP rotation of a value within each 16-lane row (row_ror:n, n = 1..15).
 template <int N>
 __device__ __forceinline__ float row_ror(float v) {

@@ -207,11 +207,47 @@ __device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs
 
 // ---------------------------------------------------------------- D1: router
 
-// Router GEMV: one wave per expert row (bf16 weights), every token.
-template <int MT, int NC>
+// Router GEMV: one wave per expert row (bf16 weights), every token.  STEP (the decoder step):
+// every workgroup first forms r = bf16(h + a) and the RMS-normalised rows n of the T tokens in
+// LDS (the order of add_rms_norm_kernel: rms_* in common.h) and reads its activations from
+// there; workgroup 0 also writes r and n for the later kernels.
+template <int MT, int NC, bool STEP>
 __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // STEP: n, [T][H]
+  __shared__ float wsum[4];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
   const int e = blockIdx.x * 4 + wave;
+  if (STEP) {
+    const int nch = p.H / 8;
+    const bool publish = blockIdx.x == 0;
+    float part[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      part[t] = 0.0f;
+      if (t >= p.T) continue;
+      for (int c = threadIdx.x; c < nch; c += 256) {
+        const int64_t o = (int64_t)t * p.H + 8 * c;
+        const u32x4 r = rms_residual(*(const u32x4 *)(p.h_in + o), p.a_in ? (const u32x4 *)(p.a_in + o) : nullptr);
+        *(u32x4 *)(xs + o) = r;
+        if (publish) *(u32x4 *)(p.r_out + o) = r;
+        part[t] = rms_partial(r, part[t]);
+      }
+    }
+    float inv[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) inv[t] = t < p.T ? rms_inverse(rms_total(part[t], wsum), p.H, p.eps) : 0.0f;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      if (t >= p.T) continue;
+      for (int c = threadIdx.x; c < nch; c += 256) {
+        const int64_t o = (int64_t)t * p.H + 8 * c;
+        const u32x4 n = rms_apply(*(const u32x4 *)(xs + o), *(const u32x4 *)(p.norm_w + 8 * c), inv[t]);
+        *(u32x4 *)(xs + o) = n;
+        if (publish) *(u32x4 *)(p.x_out + o) = n;
+      }
+    }
+    __syncthreads();
+  }
   if (e >= p.E) return;
   const int nchunks = p.H / 32;
   const uint16_t *w = p.router_w + (int64_t)e * p.H;
@@ -230,7 +266,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) 
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       const int tr = t < p.T ? t : p.T - 1;
-      const u32x4 *xp = (const u32x4 *)(p.x + (int64_t)tr * p.H + c * 32);
+      const u32x4 *xp = (const u32x4 *)((STEP ? xs : p.x) + (int64_t)tr * p.H + c * 32);
 #pragma unroll
       for (int i = 0; i < 4; ++i) xv[t][i] = xp[i];
     }
@@ -423,6 +459,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   const bool has_shared = p.Is > 0;
   // loads the combine needs, issued first (a missing shared expert reads a score instead)
   const uint16_t zbits = has_shared ? p.z[t] : p.scores[0];
+  const uint16_t rbits = p.ffn_out ? p.r_out[(int64_t)t * p.H + h] : 0;  // the decoder step's residual
   float sc[KM];
 #pragma unroll
   for (int j = 0; j < KM; ++j) sc[j] = bf2f(p.scores[t * p.k + (j < p.k ? j : p.k - 1)]);
@@ -511,6 +548,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   if (has_shared) out = shared_gated_add(sparse, vals[q][KM], round_bf(det_sigmoid(bf2f(zbits))));
   p.sparse[(int64_t)t * p.H + h] = (uint16_t)sparse;
   p.y[(int64_t)t * p.H + h] = (uint16_t)out;
+  if (p.ffn_out) p.ffn_out[(int64_t)t * p.H + h] = (uint16_t)f2bf(bf2f(rbits) + bf2f(out));
 }
 
 // 256-thread launch; ev (nullable) = {start, stop} events recorded around the kernel itself
@@ -573,7 +611,15 @@ void launch_down(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
 
 template <int MT, int NC>
 void launch_router_nc(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
-  launch_timed(decode_router_kernel<MT, NC>, dim3(blocks), s, ev, a);
+  if (!a.norm_w) {
+    launch_timed(decode_router_kernel<MT, NC, false>, dim3(blocks), s, ev, a);
+    return;
+  }
+  const size_t lds = (size_t)a.T * a.H * 2;
+  if (ev)
+    hipExtLaunchKernelGGL(decode_router_kernel<MT, NC, true>, dim3(blocks), dim3(256), lds, s, ev[0], ev[1], 0, a);
+  else
+    hipLaunchKernelGGL((decode_router_kernel<MT, NC, true>), dim3(blocks), dim3(256), lds, s, a);
 }
 
 template <int MT>
@@ -591,7 +637,9 @@ bool decode_supported(const DecodeArgs &a) {
          (a.dn_bits == 4 || a.dn_bits == 8) && a.gu_group >= 32 && a.dn_group >= 32 &&
          (a.Is == 0 || (a.sd_bits == a.dn_bits && (a.sg_bits == 4 || a.sg_bits == 8) &&
                         (a.sz_bits == 4 || a.sz_bits == 8) && a.sd_group >= 32 &&
-                        a.sg_group >= 32 && a.sz_group >= 32));
+                        a.sg_group >= 32 && a.sz_group >= 32)) &&
+         (!a.norm_w || ((size_t)a.T * a.H * 2 <= (size_t)kDecodeStepLds && a.H % 8 == 0 && a.h_in &&
+                        a.r_out && a.x_out && a.x == a.x_out && a.ffn_out));
 }
 
 hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, const hipEvent_t *kev) {

@@ -247,9 +247,10 @@ __global__ __launch_bounds__(256) void add_bf16_kernel(const uint16_t *__restric
 // The decoder's RMSNorm input of the block (decoder_layer_forward.rs:111-116 with MLX
 // fast::rms_norm): r = bf16(h + a) (a may be null: r = h), n = bf16(w * bf16(r * inv)) with
 // inv = 1 / sqrt(mean(r^2) + eps) in fp32 (IEEE sqrt and division).  mean(r^2) in a fixed
-// order the host oracle repeats: thread j of the 256 sums r_i^2 for i = j, j + 256, ... in
-// turn, each wave combines its lanes by the canonical butterfly (wave_sum) and the four wave
-// sums add as (w0 + w1) + (w2 + w3).  One workgroup per token row.
+// order the host oracle and the decode router kernel repeat (rms_partial / rms_total in
+// common.h): thread j of 256 owns the 8-element chunks j, j + 256, ... and sums their r^2 in
+// element order; each wave combines its lanes by the canonical butterfly and the four wave sums
+// add as (w0 + w1) + (w2 + w3).  One workgroup per token row; H a multiple of 8.
 template <int PER>
 __global__ __launch_bounds__(256) void add_rms_norm_kernel(const uint16_t *__restrict__ h,
                                                            const uint16_t *__restrict__ a,
@@ -259,30 +260,25 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(const uint16_t *__res
 #pragma clang fp contract(off)
   __shared__ float wsum[4];
   const int64_t row = (int64_t)blockIdx.x * H;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  float rv[PER];
+  const int tid = threadIdx.x;
+  const int nch = H / 8;
+  u32x4 rv[PER];
   float part = 0.0f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int e = tid + 256 * i;
-    float v = 0.0f;
-    if (e < H) {
-      v = bf2f(h[row + e]);
-      if (a) v = round_bf(v + bf2f(a[row + e]));
-      if (r_out) r_out[row + e] = (uint16_t)f2bf(v);
+    const int c = tid + 256 * i;
+    rv[i] = u32x4{0u, 0u, 0u, 0u};
+    if (c < nch) {
+      rv[i] = rms_residual(*(const u32x4 *)(h + row + 8 * c), a ? (const u32x4 *)(a + row + 8 * c) : nullptr);
+      if (r_out) *(u32x4 *)(r_out + row + 8 * c) = rv[i];
+      part = rms_partial(rv[i], part);
     }
-    rv[i] = v;
-    part = part + v * v;
   }
-  const float ws = wave_sum(part);
-  if (lane == 0) wsum[wave] = ws;
-  __syncthreads();
-  const float total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-  const float inv = 1.0f / __builtin_sqrtf(total / (float)H + eps);
+  const float inv = rms_inverse(rms_total(part, wsum), H, eps);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int e = tid + 256 * i;
-    if (e < H) n_out[row + e] = (uint16_t)f2bf(bf2f(w[e]) * round_bf(rv[i] * inv));
+    const int c = tid + 256 * i;
+    if (c < nch) *(u32x4 *)(n_out + row + 8 * c) = rms_apply(rv[i], *(const u32x4 *)(w + 8 * c), inv);
   }
 }
 
@@ -371,12 +367,11 @@ __global__ __launch_bounds__(256) void laguna_route_kernel(const uint16_t *__res
 hipError_t launch_add_rms_norm(const uint16_t *h, const uint16_t *a, const uint16_t *w, float eps, int T,
                                int H, uint16_t *r_out, uint16_t *n_out, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  const int per = (H + 255) / 256;
+  const int per = (H / 8 + 255) / 256;
 #define ASTRO_RMS(P) hipLaunchKernelGGL(add_rms_norm_kernel<P>, dim3(T), dim3(256), 0, s, h, a, w, eps, H, r_out, n_out)
-  if (per <= 4) ASTRO_RMS(4);
-  else if (per <= 8) ASTRO_RMS(8);
-  else if (per <= 16) ASTRO_RMS(16);
-  else ASTRO_RMS(32);
+  if (per <= 1) ASTRO_RMS(1);
+  else if (per <= 2) ASTRO_RMS(2);
+  else ASTRO_RMS(4);
 #undef ASTRO_RMS
   return hipGetLastError();
 }

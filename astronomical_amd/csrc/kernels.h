@@ -126,7 +126,16 @@ struct DecodeArgs {
   int64_t act_ld;
   uint16_t *sparse, *y;  // outputs: weighted sum of the routed experts, block output
   int router_blocks, shared_pair_blocks, max_groups;
+  // decoder step (norm_w set): the router kernel forms r = bf16(h_in + a_in) (a_in nullable)
+  // and the RMS-normalised rows itself (its first workgroup writes them to r_out and x_out; x
+  // must be x_out), and the down kernel also writes ffn_out = bf16(r + y)
+  const uint16_t *h_in, *a_in, *norm_w;
+  float eps;
+  uint16_t *r_out, *x_out, *ffn_out;
 };
+// the router kernel keeps the T normalised rows in LDS: the decoder step fuses into the decode
+// kernels when T * H * 2 bytes fit
+constexpr int kDecodeStepLds = 60 * 1024;
 
 bool decode_supported(const DecodeArgs &a);
 constexpr int kDecodeRowsPerWave = 1;  // must match kRowsPerWave in decode.hip

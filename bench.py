@@ -369,12 +369,18 @@ def decoder_step(CF, DS, ops, torch, blocks, K, W):
     dec_us = e0.elapsed_time(e1) / K / nL * 1000
 
     def timed(fn, iters=10):
+        """device time of fn, replayed from a graph of `iters` calls (no host launch cost)"""
         fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(iters):
+                fn()
+        gr.replay()
         torch.cuda.synchronize()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0.record()
-        for _ in range(iters):
-            fn()
+        gr.replay()
         t1.record()
         torch.cuda.synchronize()
         return t0.elapsed_time(t1) / iters * 1000

@@ -618,14 +618,16 @@ done:
  * division.  MLX computes the normaliser in fp32, rounds x * inv to the input dtype and
  * multiplies by the weight in that dtype (its fast::rms_norm fallback); the order of the
  * fp32 sum of squares inside MLX is not pinned.  This restatement fixes it: partial j of 256
- * sums r_i^2 for i = j, j + 256, ... in turn; the partials of each group of 64 combine by the
- * butterfly of the softmax denominator, and the four group sums as (g0 + g1) + (g2 + g3).
+ * owns the 8-element chunks j, j + 256, ... and sums their r_i^2 in element order; the
+ * partials of each group of 64 combine by the butterfly of the softmax denominator, and the
+ * four group sums as (g0 + g1) + (g2 + g3).  H is a multiple of 8.
  */
 static void rms_norm_row(const float *r, const uint16_t *w, float eps, int32_t H, uint16_t *n) {
   float part[256];
   for (int j = 0; j < 256; ++j) {
     float p = 0.0f;
-    for (int32_t i = j; i < H; i += 256) p = p + r[i] * r[i];
+    for (int32_t c = j; c * 8 < H; c += 256)
+      for (int32_t i = 8 * c; i < 8 * c + 8; ++i) p = p + r[i] * r[i];
     part[j] = p;
   }
   float g[4];
@@ -646,7 +648,7 @@ static void rms_norm_row(const float *r, const uint16_t *w, float eps, int32_t H
 
 int orc_add_rms_norm(const uint16_t *h, const uint16_t *a, const uint16_t *w, float eps, int32_t T,
                      int32_t H, uint16_t *r_out, uint16_t *n_out) {
-  if (T < 0 || H <= 0) return ORC_ERR_GEOMETRY;
+  if (T < 0 || H <= 0 || H % 8 != 0) return ORC_ERR_GEOMETRY;
   int err = ORC_OK;
 #pragma omp parallel num_threads(g_threads)
   {
