@@ -111,6 +111,9 @@ EXPORTS = {
     "astro_moe_block_forward_attributed": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p,
                                             C.c_void_p, C.c_size_t, C.c_void_p,
                                             C.POINTER(C.c_float)], C.c_int),
+    "astro_moe_verification_workspace_bytes": ([C.POINTER(Layer), C.c_int32, C.POINTER(C.c_size_t)], C.c_int),
+    "astro_moe_block_forward_verification": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                                              C.c_size_t, C.c_void_p], C.c_int),
     "astro_moe_router_logits": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
     "astro_moe_route_topk": ([C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                               C.c_void_p, C.c_void_p], C.c_int),
@@ -123,6 +126,9 @@ EXPORTS = {
                               C.c_int32, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "astro_moe_quantized_matmul": ([C.c_void_p, C.c_int32, C.POINTER(Affine), C.c_void_p,
                                     C.c_void_p], C.c_int),
+    "astro_moe_verification_quantized_linear": ([C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                                 C.POINTER(Affine), C.c_int32, C.c_void_p, C.c_void_p],
+                                                C.c_int),
     "astro_moe_swiglu": ([C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
     "astro_moe_sorted_weighted_sum": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                        C.c_int32, C.c_void_p, C.c_void_p], C.c_int),

@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libastro_moe.so")
-SOURCES = ["abi.hip", "gemm.hip", "route.hip", "decode.hip", "elementwise.hip", "synth.hip", "pages.hip"]
+SOURCES = ["abi.hip", "gemm.hip", "route.hip", "decode.hip", "elementwise.hip", "synth.hip", "pages.hip", "verify.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "--offload-arch=gfx950", "-fPIC", "-std=c++17", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -459,7 +459,7 @@ struct DecoderStep {
 
 int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, uint16_t *y,
               void *workspace, size_t workspace_bytes, void *stream, StageClock *clock,
-              const DecoderStep *step = nullptr) {
+              const DecoderStep *step = nullptr, bool verification = false) {
   int rc = check_layer(kBlockOp, layer);
   if (rc) return rc;
   if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
@@ -599,6 +599,7 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
       d.x_out = step->n;
       d.ffn_out = step->out;
     }
+    d.unsorted = verification;
     if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
     // kernel-attached events: router | gate/up (shared gate/up, routing, sort inside) |
     // down (shared down and the combine inside)
@@ -682,6 +683,41 @@ int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
 int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
                             uint16_t *y, void *workspace, size_t workspace_bytes, void *stream) {
   return run_block(layer, x, tokens, y, workspace, workspace_bytes, stream, nullptr);
+}
+
+// forward_moe_resident_target_verification (resident_execution.rs:146-208): the rows of an MTP
+// verification window stay unsorted, so each output row equals the one-token block of its row
+// (the rollback boundary after a rejected draft).  The window runs in pieces the decode kernels
+// take whole (at most 8 tokens and 64 assignments, unsorted combine), or one token at a time
+// when they do not apply.
+int astro_moe_block_forward_verification(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                                         uint16_t *y, void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = check_layer(kBlockOp, layer);
+  if (rc) return rc;
+  if (tokens < 0) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count must not be negative");
+  if (tokens == 0) return ok();
+  if (!x || !y) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "hidden states and output must be non-null");
+  const astro_moe_layer &L = *layer;
+  int piece = std::max(1, std::min({8, 64 / std::max(1, L.top_k), (int)tokens}));
+  if (!decode_path(L, piece)) piece = 1;
+  const int64_t H = L.hidden;
+  for (int32_t t0 = 0; t0 < tokens; t0 += piece) {
+    const int32_t n = std::min<int32_t>(piece, tokens - t0);
+    rc = run_block(layer, x + t0 * H, n, y + t0 * H, workspace, workspace_bytes, stream, nullptr, nullptr, true);
+    if (rc) return rc;
+  }
+  return ok();
+}
+
+int astro_moe_verification_workspace_bytes(const astro_moe_layer *layer, int32_t tokens, size_t *bytes) {
+  int rc = check_layer(kBlockOp, layer);
+  if (rc) return rc;
+  if (tokens < 0 || !bytes) return fail(ASTRO_MOE_INVALID_ARGUMENT, kBlockOp, "token count and output must be valid");
+  const astro_moe_layer &L = *layer;
+  int piece = std::max(1, std::min({8, 64 / std::max(1, L.top_k), (int)std::max(tokens, 1)}));
+  if (!decode_path(L, piece)) piece = 1;
+  *bytes = block_layout(L, piece, L.top_k, true).total;
+  return ok();
 }
 
 int astro_moe_block_forward_attributed(const astro_moe_layer *layer, const uint16_t *x,
@@ -856,7 +892,11 @@ int astro_moe_quantized_matmul(const uint16_t *x, int32_t rows, const astro_moe_
   if (!x || !out) return fail(ASTRO_MOE_INVALID_ARGUMENT, kQmmOp, "quantized matmul buffers must be non-null");
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
-  if (w->out_features < 16) {
+  if (rows <= kVerifyRows && verify_qmv_supported(w->in_features, w->bits, w->group_size, x, w->w)) {
+    // a few rows: the multi-token QMV (each row's bits are those of a one-row call)
+    e = launch_verify_qmv(x, rows, w->in_features, w->w, w->scales, w->biases, w->out_features, w->bits,
+                          w->group_size, false, out, s);
+  } else if (w->out_features < 16) {
     e = launch_qgemv_rows(x, rows, w->in_features, w->w, w->scales, w->biases, w->out_features,
                           w->bits, w->group_size, out, s);
   } else {
@@ -873,6 +913,42 @@ int astro_moe_quantized_matmul(const uint16_t *x, int32_t rows, const astro_moe_
     e = launch_grouped_gemm(g, kEpiPlain, s);
   }
   return e == hipSuccess ? ok() : hip_fail(kQmmOp, e);
+}
+
+// qwen3_5_target_verification_quantized_linear (target_verification_quantized_linear.rs:232-330)
+// with the checks of validate_target_verification_projection (:378-447).  One kernel serves
+// both of the reference's dispatch arms: its outputs are token-local by construction.
+int astro_moe_verification_quantized_linear(const void *activations, int32_t batch, int32_t tokens,
+                                            int32_t in_features, const astro_moe_affine *w, int32_t dtype,
+                                            void *out, void *stream) {
+  const char *op = "project Qwen3.5 target-verification tokens";
+  if (batch <= 0 || tokens <= 0 || in_features <= 0 || !w || w->experts != 1 || w->out_features <= 0 ||
+      w->in_features <= 0 || ((int64_t)w->in_features * w->bits) / 32 <= 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op,
+                "target-verification arrays must have positive rank-three activations and rank-two weights");
+  if ((w->group_size != 32 && w->group_size != 64 && w->group_size != 128) ||
+      (w->bits != 2 && w->bits != 3 && w->bits != 4 && w->bits != 5 && w->bits != 6 && w->bits != 8))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "target-verification affine metadata is not supported by MLX");
+  if (((int64_t)w->in_features * w->bits) % 32 != 0 || w->in_features != in_features ||
+      in_features % w->group_size != 0)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op,
+                "target-verification affine arrays do not match activation and weight geometry");
+  if (!activations || !out || !w->w || !w->scales || !w->biases)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "target-verification buffers must be non-null");
+  if (dtype != ASTRO_MOE_DTYPE_BF16 && dtype != ASTRO_MOE_DTYPE_F16)
+    return fail(ASTRO_MOE_UNSUPPORTED, op,
+                "the verification kernel reads bfloat16 or float16 activations, scales and biases");
+  if ((int64_t)batch * tokens > (int64_t)INT32_MAX / in_features)
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "target-verification activations are too large");
+  if (!verify_qmv_supported(in_features, w->bits, w->group_size, activations, w->w))
+    return fail(ASTRO_MOE_UNSUPPORTED, op,
+                "the verification kernel needs 4-, 5- or 8-bit codes, an input width that is a multiple of "
+                "128 and 16-byte aligned activations and codes");
+  const hipError_t e =
+      launch_verify_qmv((const uint16_t *)activations, batch * tokens, in_features, w->w, w->scales, w->biases,
+                        w->out_features, w->bits, w->group_size, dtype == ASTRO_MOE_DTYPE_F16, (uint16_t *)out,
+                        (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(op, e);
 }
 
 int astro_moe_swiglu(const uint16_t *gate, const uint16_t *up, int64_t n, uint16_t *out,

@@ -582,8 +582,9 @@ void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev)
 template <int BITS, int NC>
 void launch_down_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   const dim3 grid(a.H / 4, a.T);
-  // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64
-  if (a.A >= 64)
+  // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64; a verification
+  // window keeps the unsorted one (resident_execution.rs:161-162)
+  if (a.A >= 64 && !a.unsorted)
     launch_timed(decode_down_kernel<BITS, NC, true>, grid, s, ev, a);
   else
     launch_timed(decode_down_kernel<BITS, NC, false>, grid, s, ev, a);

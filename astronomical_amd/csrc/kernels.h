@@ -72,6 +72,16 @@ hipError_t launch_qgemv_rows(const uint16_t *x, int T, int K, const uint32_t *w,
                              const uint16_t *sc, const uint16_t *bi, int N, int bits, int group,
                              uint16_t *out, hipStream_t s);
 
+// Multi-token quantized linear (target-verification windows and small-batch quantized
+// matmul): y[m] = x[m] . deq(W)^T for M token rows, bf16 or f16 activations / scales /
+// biases / outputs, 4-, 5- or 8-bit codes.  One launch per kVerifyRows rows; every output
+// has the bits it has at M = 1.
+constexpr int kVerifyRows = 16;
+bool verify_qmv_supported(int K, int bits, int group, const void *x, const void *w);
+hipError_t launch_verify_qmv(const uint16_t *x, int M, int K, const uint32_t *w, const uint16_t *sc,
+                             const uint16_t *bi, int N, int bits, int group, bool f16, uint16_t *y,
+                             hipStream_t s);
+
 hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *out,
                          hipStream_t s);
 
@@ -132,6 +142,8 @@ struct DecodeArgs {
   const uint16_t *h_in, *a_in, *norm_w;
   float eps;
   uint16_t *r_out, *x_out, *ffn_out;
+  // target-verification windows: the unsorted combine at every A (token-local rows)
+  bool unsorted;
 };
 // the router kernel keeps the T normalised rows in LDS: the decoder step fuses into the decode
 // kernels when T * H * 2 bytes fit

@@ -213,6 +213,84 @@ def quantized_matmul_affine(activations: torch.Tensor, weights: AffineWeights) -
     return out.reshape(*x.shape[:-1], w.out_features)
 
 
+# ------------------------------------------------- MTP target verification (target_verification_quantized_linear.rs)
+
+class TargetVerificationProjectionDispatch(Enum):
+    """Qwen3_5TargetVerificationProjectionDispatch (target_verification_quantized_linear.rs:180-186):
+    the arm the reference picks from the geometry.  Here one kernel serves both arms with the
+    same token-local arithmetic; the classification is kept for callers that report it."""
+
+    OPTIMIZED_METAL = "OptimizedMetal"
+    TOKEN_LOCAL_MLX_FALLBACK = "TokenLocalMlxFallback"
+
+
+@dataclass
+class TargetVerificationProjection:
+    """Qwen3_5TargetVerificationProjection (:188-207)."""
+
+    projected_activations: torch.Tensor
+    dispatch: TargetVerificationProjectionDispatch
+
+    def into_projected_activations(self) -> torch.Tensor:
+        return self.projected_activations
+
+
+def target_verification_uses_optimized_dispatch(activation_dtype: torch.dtype, scale_dtype: torch.dtype,
+                                                bias_dtype: torch.dtype, group_size: int, bits: int,
+                                                input_dimension: int, output_dimension: int) -> bool:
+    """target_verification_uses_optimized_dispatch (:332-356)."""
+    return (bits in (4, 5) and group_size in (32, 64, 128) and input_dimension > 0
+            and input_dimension % 512 == 0 and output_dimension > 0 and output_dimension % 8 == 0
+            and activation_dtype == scale_dtype and bias_dtype == scale_dtype
+            and activation_dtype in (torch.bfloat16, torch.float16))
+
+
+_VERIFY_DTYPES = {torch.bfloat16: _lib.DTYPES.index("BF16"), torch.float16: _lib.DTYPES.index("F16")}
+
+
+def qwen3_5_target_verification_quantized_linear(activations: torch.Tensor, packed_weight: torch.Tensor,
+                                                 quantization_scales: torch.Tensor,
+                                                 quantization_biases: torch.Tensor,
+                                                 quantization_group_size: int,
+                                                 quantization_bits: int) -> TargetVerificationProjection:
+    """qwen3_5_target_verification_quantized_linear (:232-330): activations [B, T, K] (bf16 or
+    f16), packed_weight [N, K * bits / 32] (uint32 bits as int32), scales / biases [N, K / g] of
+    the activations' dtype -> [B, T, N] of that dtype.  Each token row's output has the bits of
+    projecting that row alone."""
+    op = "project Qwen3.5 target-verification tokens"
+    a_shape, w_shape = tuple(activations.shape), tuple(packed_weight.shape)
+    if len(a_shape) != 3 or min(a_shape) <= 0 or len(w_shape) != 2 or min(w_shape) <= 0:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, f"{op}: target-verification arrays must have positive "
+                            "rank-three activations and rank-two weights")
+    if packed_weight.dtype != torch.int32 or quantization_group_size not in (32, 64, 128) \
+            or quantization_bits not in (2, 3, 4, 5, 6, 8):
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, f"{op}: target-verification affine metadata is not "
+                            "supported by MLX")
+    K, N = a_shape[2], w_shape[0]
+    expanded = w_shape[1] * 32 // quantization_bits if (w_shape[1] * 32) % quantization_bits == 0 else None
+    affine_shape = (N, K // quantization_group_size)
+    if expanded != K or K % quantization_group_size or tuple(quantization_scales.shape) != affine_shape \
+            or tuple(quantization_biases.shape) != affine_shape:
+        raise AstroMoeError(_lib.INVALID_ARGUMENT, f"{op}: target-verification affine arrays do not match "
+                            "activation and weight geometry")
+    dtype = activations.dtype
+    if dtype not in _VERIFY_DTYPES or quantization_scales.dtype != dtype or quantization_biases.dtype != dtype:
+        raise AstroMoeError(_lib.UNSUPPORTED, f"{op}: the verification kernel reads bfloat16 or float16 "
+                            "activations, scales and biases")
+    dispatch = (TargetVerificationProjectionDispatch.OPTIMIZED_METAL
+                if target_verification_uses_optimized_dispatch(dtype, quantization_scales.dtype,
+                                                               quantization_biases.dtype,
+                                                               quantization_group_size, quantization_bits, K, N)
+                else TargetVerificationProjectionDispatch.TOKEN_LOCAL_MLX_FALLBACK)
+    x = activations.contiguous()
+    w = Affine(packed_weight.data_ptr(), quantization_scales.contiguous().data_ptr(),
+               quantization_biases.contiguous().data_ptr(), 1, N, K, quantization_bits, quantization_group_size)
+    out = torch.empty(a_shape[0], a_shape[1], N, dtype=dtype, device=x.device)
+    call("astro_moe_verification_quantized_linear", _ptr(x), a_shape[0], a_shape[1], K, C.byref(w),
+         _VERIFY_DTYPES[dtype], _ptr(out), _stream(x.device))
+    return TargetVerificationProjection(out, dispatch)
+
+
 def apply_compiled_swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """mlx_compiled_swiglu.rs:44-89: silu(gate) * up in bf16."""
     g, u = gate.contiguous(), up.contiguous()
@@ -320,6 +398,23 @@ class MoeBlock:
         return y
 
     __call__ = forward
+
+    def target_verification_forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                                    workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """forward_moe_resident_target_verification (resident_execution.rs:146-208): the block
+        over an MTP verification window, each output row bit-equal to the one-token block of
+        its row."""
+        x2 = x.contiguous().view(torch.bfloat16).reshape(-1, self.weights.hidden)
+        T = x2.shape[0]
+        y = out if out is not None else torch.empty_like(x2)
+        n = C.c_size_t()
+        call("astro_moe_verification_workspace_bytes", C.byref(self._struct), T, C.byref(n))
+        ws = workspace
+        if ws is None or ws.numel() < n.value:
+            ws = torch.empty(max(n.value, 1), dtype=torch.uint8, device=self.device)
+        call("astro_moe_block_forward_verification", C.byref(self._struct), _ptr(x2), T, _ptr(y), _ptr(ws),
+             ws.numel(), _stream(self.device))
+        return y
 
     def decoder_feed_forward(self, hidden: torch.Tensor, norm_weight: torch.Tensor, eps: float,
                              attention_out: Optional[torch.Tensor] = None,

@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the side measurements of configs c3 and c4")
+    p.add_argument("--verification-only", action="store_true",
+                   help="only the MTP verification QMV measurement (one JSON line of its own)")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--copy-check", action="store_true",
                    help="run a 1 GiB streaming copy first (counter calibration)")
@@ -72,6 +74,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.verification_only:
+        print(json.dumps(verification_qmv(CF, DS, ops, torch)))
+        return
     if args.copy_check:
         # a plain streaming kernel of known traffic: reads 1 GiB, writes 1 GiB
         a = torch.ones(1 << 28, dtype=torch.float32, device=dev)
@@ -200,6 +205,7 @@ def main():
     if not args.no_extra:
         extra = decoder_step(CF, DS, ops, torch, blocks, K, W)
         extra.update(other_configs(CF, DS, ops, torch, K, W, layers[0]))
+        extra["verification_lm_head"] = verification_qmv(CF, DS, ops, torch)
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
@@ -332,6 +338,51 @@ def other_configs(CF, DS, ops, torch, K, W, layer_c1):
     del L4, b4, ws4
     torch.cuda.empty_cache()
     log(f"other configs: {json.dumps(out)}")
+    return out
+
+
+def verification_qmv(CF, DS, ops, torch, reps=20, vocab=248_320):
+    """The multi-token QMV of MTP target-verification windows on the largest linear that runs
+    through it: the c1 model's logits head (hidden 2048 -> vocabulary 248,320, the Qwen3.5-MoE
+    config of the reference's tests), 4-bit and 5-bit g64, for windows of 1..16 tokens.  A
+    hipGraph of `reps` launches per point, timed with events; bytes = codes + scales + biases
+    + activations + outputs (one pass over the weights per launch)."""
+    H = CF.C1.hidden
+    out = {"workload": f"MTP verification window (batch 1, T tokens) through the logits head "
+                       f"{H} -> {vocab}, bf16 activations, affine g64 codes; one launch per window"}
+    for bits in (4, 5):
+        cfg = CF.C1.with_(bits=bits)
+        w = DS.affine(cfg, cfg.seed, f"lm_head_{bits}", 1, vocab, H)
+        codes, sc, bi = w.w[0], w.scales[0], w.biases[0]
+        res = {}
+        for T in (1, 2, 4, 8, 16):
+            x = DS.normal_bf16(cfg.seed, f"verify_x_{T}", (1, T, H), 1.0)
+
+            def fn():
+                ops.qwen3_5_target_verification_quantized_linear(x, codes, sc, bi, cfg.group_size, bits)
+            fn()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(reps):
+                    fn()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000 / reps
+            nbytes = vocab * H * bits // 8 + vocab * (H // cfg.group_size) * 4 + T * H * 2 + T * vocab * 2
+            gbs = nbytes / (us * 1e-6) / 1e9
+            res[f"T{T}"] = {"us": round(us, 2), "bytes": int(nbytes), "GBps": round(gbs, 1),
+                            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            del g
+        out[f"{bits}bit"] = res
+        del w, codes, sc, bi
+        torch.cuda.empty_cache()
+    log(f"verification qmv: {json.dumps(out)}")
     return out
 
 

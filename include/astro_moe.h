@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ASTRO_MOE_ABI_VERSION 3
+#define ASTRO_MOE_ABI_VERSION 4
 
 enum astro_moe_status {
   ASTRO_MOE_OK = 0,
@@ -158,6 +158,17 @@ int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int
 int astro_moe_block_forward_attributed(const astro_moe_layer *layer, const uint16_t *x,
                                        int32_t tokens, uint16_t *y, void *workspace,
                                        size_t workspace_bytes, void *stream, float *stage_ms);
+
+/*
+ * The block over an MTP target-verification window (forward_moe_resident_target_verification,
+ * resident_execution.rs:146-208): token rows stay unsorted, so output row t has the bits of
+ * astro_moe_block_forward on row t alone, whatever the window length (the exact rollback
+ * boundary after a rejected draft).  Same arguments as astro_moe_block_forward; the
+ * workspace is astro_moe_verification_workspace_bytes(layer, tokens).
+ */
+int astro_moe_verification_workspace_bytes(const astro_moe_layer *layer, int32_t tokens, size_t *bytes);
+int astro_moe_block_forward_verification(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                                         uint16_t *y, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Router projection logits = x·W_rᵀ (bf16 out, fp32 accumulate), plus router_bias if
  * set: forward.rs:52-93 (matmul or quantized_linear). */
@@ -385,6 +396,25 @@ int astro_moe_build_expert_page_manifest(const astro_moe_expert_layer_plan *plan
 int astro_moe_load_expert_page(const astro_moe_expert_layer_plan *plan, const int32_t *expert_ids,
                                int32_t n, int32_t fuse_gate_up, void *const *dst, int32_t dst_on_device,
                                void *staging, size_t staging_bytes, void *stream, uint64_t *bytes_read);
+
+/*
+ * ------------------------------------------------------------------ multi-token QMV for MTP verification
+ * qwen3_5_target_verification_quantized_linear (qwen3_5/model/target_verification_quantized_linear.rs:
+ * 232-330), the quantized linear of an MTP target-verification window (router, shared expert,
+ * attention and logits projections; :453-488):
+ *   out[b][t][n] = sum_k activations[b][t][k] * (s[n][k/g] * q[n][k] + b[n][k/g])
+ * activations [batch][tokens][in_features], out [batch][tokens][w.out_features], and w's scales and
+ * biases all of `dtype` (ASTRO_MOE_DTYPE_BF16 or ASTRO_MOE_DTYPE_F16); w.experts == 1, codes u32
+ * [out_features][in_features * bits / 32] LSB-first.  fp32 accumulation, one rounding to dtype.
+ * Every output row equals the one-token projection of its own activation row bit for bit (the
+ * reference's token-local contract, :333-356); for bf16 that is astro_moe_quantized_matmul of
+ * that row.  Errors: validate_target_verification_projection (:378-447), then status 2 for
+ * 2/3/6-bit codes, dtypes other than bf16/f16, in_features not a multiple of 128, or
+ * activations or codes not 16-byte aligned.
+ */
+int astro_moe_verification_quantized_linear(const void *activations, int32_t batch, int32_t tokens,
+                                            int32_t in_features, const astro_moe_affine *w, int32_t dtype,
+                                            void *out, void *stream);
 
 /*
  * Seeded synthetic inputs for benchmarks and tests (no counterpart in the reference):

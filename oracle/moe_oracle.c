@@ -35,6 +35,12 @@
  *                        unit RMS of the unweighted output, eps dominance;
  *                        tests/test_oracle_decoder.py
  *   orc_decoder_ffn_forward  composition (residual add, RMS norm, block, residual add)
+ *   orc_f32_to_f16 / orc_f16_to_f32  IEEE binary16 round to nearest even; tests/test_oracle_verify.py
+ *                        (numpy float16 conversion over random, subnormal, overflow and tie patterns)
+ *   orc_verification_quantized_linear  fp64 dequantize+matmul brute force on the reference's test
+ *                        geometries (target_verification_quantized_linear.rs tests, 4/5-bit, bf16/f16);
+ *                        4- and 5-bit code order checked against the reference QMV's byte masks
+ *                        (target_verification_quantized_linear.rs:63-90); tests/test_oracle_verify.py
  *   orc_laguna_route     reference KATs laguna_hermetic/routing.rs:8-60 (bias selects only,
  *                        ties to the lower id, softcap before sigmoid, normalisation) and
  *                        direct_mlx/laguna/routing.rs:63-122 ([0, 1] with bias); fp64 brute force
@@ -76,6 +82,42 @@ float orc_bf16_to_f32(uint16_t h) {
 
 static inline float bf(uint16_t h) { return orc_bf16_to_f32(h); }
 static inline uint16_t tobf(float f) { return orc_f32_to_bf16(f); }
+
+/* IEEE binary16 from binary32, round to nearest even (subnormals, overflow to infinity). */
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds past 65504 */
+  const int32_t e = (int32_t)(a >> 23) - 127;
+  if (e >= -14) {
+    const uint32_t m = a & 0x7fffffu, rest = m & 0x1fffu;
+    uint32_t h = ((uint32_t)(e + 15) << 10) | (m >> 13);
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+  }
+  if (e < -25) return (uint16_t)sign;
+  /* subnormal: value in units of 2^-24 is the 24-bit significand shifted right by -(e + 1) */
+  const uint32_t m = (a & 0x7fffffu) | 0x800000u;
+  const int32_t sh = -(e + 1);
+  uint32_t h = m >> sh;
+  const uint32_t rest = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+  if (rest > half || (rest == half && (h & 1u))) h += 1u;
+  return (uint16_t)(sign | h);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  float f;
+  if (e == 0) {
+    f = ldexpf((float)m, -24);
+    return sign ? -f : f;
+  }
+  const uint32_t u = sign | (e == 31 ? 0x7f800000u : (e + 112u) << 23) | (m << 13);
+  memcpy(&f, &u, 4);
+  return f;
+}
 
 /*
  * exp(x) for the softmax and sigmoid: Cody–Waite reduction x = n*ln2 + r with
@@ -292,7 +334,14 @@ static int affine_valid(const orc_affine *w) {
  * [j*b, j*b + b) of the row's little-endian bit stream of u32 words (LSB first).
  * Dequantised value: scale * q + bias per group of `group_size` inputs, in fp32.
  */
+static void dequant_row_dt(const orc_affine *w, int32_t expert, int32_t n, float *out, int f16);
+
 static void dequant_row_f32(const orc_affine *w, int32_t expert, int32_t n, float *out) {
+  dequant_row_dt(w, expert, n, out, 0);
+}
+
+/* scales and biases read as bf16 (f16 == 0) or IEEE binary16 */
+static void dequant_row_dt(const orc_affine *w, int32_t expert, int32_t n, float *out, int f16) {
   const int32_t K = w->in_features;
   const int32_t words = (int32_t)(((int64_t)K * w->bits) / 32);
   const int32_t groups = K / w->group_size;
@@ -308,7 +357,8 @@ static void dequant_row_f32(const orc_affine *w, int32_t expert, int32_t n, floa
     if (shift + (uint32_t)w->bits > 32u) v |= (uint64_t)row[word + 1] << 32;
     const uint32_t q = (uint32_t)(v >> shift) & mask;
     const int32_t g = j / w->group_size;
-    out[j] = fmaf(bf(sc[g]), (float)q, bf(bi[g]));
+    out[j] = f16 ? fmaf(orc_f16_to_f32(sc[g]), (float)q, orc_f16_to_f32(bi[g]))
+                 : fmaf(bf(sc[g]), (float)q, bf(bi[g]));
   }
 }
 
@@ -403,6 +453,39 @@ int orc_gather_qmm(const uint16_t *x, const uint32_t *x_rows, int32_t rows,
   }
   memcpy(y, ys, sizeof(uint16_t) * (size_t)rows * N);
   free(xs); free(ys); free(list);
+  return ORC_OK;
+}
+
+/*
+ * qwen3_5_target_verification_quantized_linear (qwen3_5/model/target_verification_quantized_linear.rs:
+ * 232-330) over rows = batch * tokens activation rows, with the geometry checks of
+ * validate_target_verification_projection (:378-447).  Every row is projected alone, as the
+ * reference's token-local path does (:333-356): y[r][n] = round(sum_j x[r][j] * (s q + b)) with
+ * fp32 accumulation and one rounding to the activations' dtype (bf16, or binary16 when f16).
+ */
+int orc_verification_quantized_linear(const uint16_t *x, int32_t rows, const orc_affine *w, int32_t f16,
+                                      uint16_t *y) {
+  if (!affine_valid(w) || w->experts != 1 || rows <= 0) return ORC_ERR_GEOMETRY;
+  const int32_t K = w->in_features, N = w->out_features;
+#pragma omp parallel num_threads(g_threads)
+  {
+    float *wr = (float *)malloc(sizeof(float) * (size_t)K);
+    float *xr = (float *)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int32_t n = 0; n < N; ++n) {
+      dequant_row_dt(w, 0, n, wr, f16);
+      for (int32_t r = 0; r < rows; ++r) {
+        for (int32_t j = 0; j < K; ++j) {
+          const uint16_t h = x[(size_t)r * K + j];
+          xr[j] = f16 ? orc_f16_to_f32(h) : bf(h);
+        }
+        const float v = dot_f32(xr, wr, K);
+        y[(size_t)r * N + n] = f16 ? orc_f32_to_f16(v) : tobf(v);
+      }
+    }
+    free(wr);
+    free(xr);
+  }
   return ORC_OK;
 }
 

@@ -86,6 +86,8 @@ typedef struct orc_trace {
 /* scalar helpers */
 uint16_t orc_f32_to_bf16(float f);
 float orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
 float orc_expf(float x);
 void orc_set_threads(int threads);
 int orc_get_threads(void);
@@ -104,6 +106,8 @@ int orc_invert_assignment_order(const uint32_t *sorted_order, int32_t n,
 int orc_dequantize(const orc_affine *w, int32_t expert, uint16_t *out_bf16);
 int orc_qmm(const uint16_t *x, int32_t M, const orc_affine *w, int32_t expert,
             uint16_t *y);
+int orc_verification_quantized_linear(const uint16_t *x, int32_t rows, const orc_affine *w, int32_t f16,
+                                      uint16_t *y);
 int orc_gather_qmm(const uint16_t *x, const uint32_t *x_rows, int32_t rows,
                    const orc_affine *w, const uint32_t *ids, uint16_t *y);
 void orc_swiglu(const uint16_t *gate, const uint16_t *up, int64_t n, uint16_t *out);

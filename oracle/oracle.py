@@ -75,6 +75,11 @@ def lib():
         L.orc_invert_assignment_order.argtypes = [vp, i32, vp]
         L.orc_dequantize.argtypes = [C.POINTER(_Affine), i32, vp]
         L.orc_qmm.argtypes = [vp, i32, C.POINTER(_Affine), i32, vp]
+        L.orc_verification_quantized_linear.argtypes = [vp, i32, C.POINTER(_Affine), i32, vp]
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f16_to_f32.restype = C.c_float
         L.orc_gather_qmm.argtypes = [vp, vp, i32, C.POINTER(_Affine), vp, vp]
         L.orc_swiglu.argtypes = [vp, vp, i64, vp]
         L.orc_sorted_weighted_sum.argtypes = [vp, vp, vp, i32, i32, i32, vp]
@@ -180,6 +185,28 @@ def qmm(x, w, expert=0):
     y = np.empty((M, a.out_features), np.uint16)
     _check(lib().orc_qmm(_p(x), M, C.byref(a), expert, _p(y)), "quantized matmul")
     return y
+
+
+def verification_quantized_linear(x, w, f16=False):
+    """x [..., K] bf16 (or binary16 when f16) bits; w AffineWeights with one expert whose
+    scales/biases share x's dtype -> [..., N] of that dtype."""
+    keep = []
+    a = _affine(w, keep)
+    x = _c(x, np.uint16)
+    lead = x.shape[:-1]
+    x2 = np.ascontiguousarray(x.reshape(-1, x.shape[-1]))
+    y = np.empty((x2.shape[0], a.out_features), np.uint16)
+    _check(lib().orc_verification_quantized_linear(_p(x2), x2.shape[0], C.byref(a), int(bool(f16)), _p(y)),
+           "target-verification quantized linear")
+    return y.reshape(*lead, a.out_features)
+
+
+def f32_to_f16_scalar(x: float) -> int:
+    return int(lib().orc_f32_to_f16(float(x)))
+
+
+def f16_to_f32_scalar(h: int) -> float:
+    return float(lib().orc_f16_to_f32(int(h)))
 
 
 def gather_qmm(x, w, ids, x_rows=None):
