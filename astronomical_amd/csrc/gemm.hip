@@ -107,15 +107,27 @@ __device__ __forceinline__ void store_b(uint16_t *dst, const BRegs &r, bool vali
   d[3] = out[3];
 }
 
+// Workgroup -> (row tile, column tile).  Workgroups are dealt to the 8 XCDs round-robin by
+// linear id (x fastest); the grid has a multiple of 8 row tiles.  Each XCD takes the row
+// tiles x = xcd (mod 8), and its column tiles of one row tile come one after the other in
+// its dispatch order, so they run together and share the activation tile in that XCD's L2.
+__device__ __forceinline__ void tile_of_block(int &bx, int &by) {
+  const int mt = (int)gridDim.x, nb = (int)gridDim.y;
+  const int l = (int)blockIdx.x + (int)blockIdx.y * mt;
+  const int xcd = l & 7, s = l >> 3;
+  bx = (s / nb) * 8 + xcd;
+  by = s - (s / nb) * nb;
+}
+
 // Tile of the launch: blocks x < split belong to problem a, the rest to problem b (a
 // second GEMM fused into the same launch, e.g. the shared expert next to the routed
 // experts).  A problem with a tile table is grouped: x indexes its tiles; otherwise row
 // tiles are consecutive.  Returns false when the block has no work.  The problem is
 // selected by value: taking the address of a kernel argument would copy both to scratch.
-__device__ __forceinline__ bool gemm_tile(const GemmArgs &p, bool second, int split, int nblocks,
+__device__ __forceinline__ bool gemm_tile(const GemmArgs &p, int bx, int by, bool second, int split, int nblocks,
                                           int &expert, int &row0, int &m_valid) {
-  if ((int)blockIdx.y >= nblocks) return false;
-  const int x = second ? (int)blockIdx.x - split : (int)blockIdx.x;
+  if (by >= nblocks) return false;
+  const int x = second ? bx - split : bx;
   expert = 0;
   if (p.tile_expert) {
     if (x >= (int)*p.tile_count) return false;
@@ -136,11 +148,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
   __shared__ __attribute__((aligned(16))) uint16_t Bs[BR * LDSP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  const bool second = (int)blockIdx.x >= split;
+  int bx, by;
+  tile_of_block(bx, by);
+  const bool second = bx >= split;
   const GemmArgs p = second ? pb : pa;
   int expert, row0, m_valid;
-  if (!gemm_tile(p, second, split, second ? nbb : nba, expert, row0, m_valid)) return;
-  const int ntile = blockIdx.y;
+  if (!gemm_tile(p, bx, by, second, split, second ? nbb : nba, expert, row0, m_valid)) return;
+  const int ntile = by;
 
   // ---- per-thread weight row (load stage): row r = tid/2, inputs 32*half.. of a K step
   const int br = tid >> 1, half = tid & 1;
@@ -433,11 +447,13 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
                                                       int nba, int nbb) {
   extern __shared__ __attribute__((aligned(16))) char ws_lds[];
   typedef __attribute__((address_space(3))) void lds_void;
-  const bool second = (int)blockIdx.x >= split;
+  int bx, by;
+  tile_of_block(bx, by);
+  const bool second = bx >= split;
   const GemmArgs p = second ? pb : pa;
   int expert, row0, m_valid;
-  if (!gemm_tile(p, second, split, second ? nbb : nba, expert, row0, m_valid)) return;
-  const int nblk = blockIdx.y;
+  if (!gemm_tile(p, bx, by, second, split, second ? nbb : nba, expert, row0, m_valid)) return;
+  const int nblk = by;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nk = p.K / WK;
