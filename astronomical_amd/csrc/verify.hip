@@ -28,8 +28,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int VQ_WAVES = 8;
-constexpr int VQ_THREADS = 64 * VQ_WAVES;
 
 __device__ __forceinline__ float h2f(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -130,18 +128,17 @@ constexpr int vq_window() {
 
 // LDS: [ring: waves x stages x 16 rows x SPS * BITS / 4 pieces of 16 B][x fragments]
 // [group sums][scale | bias]
-template <int BITS, int MR, int G, int SPS, int NS>
+template <int BITS, int MR, int G, int SPS, int NS, int W>
 constexpr int vq_lds_bytes() {
   constexpr int KW = vq_window<G>();
-  return VQ_WAVES * NS * 64 * SPS * BITS + (KW / 32) * 4 * MR * 16 + (KW / G) * MR * 4 +
-         VQ_WAVES * 16 * (KW / G) * 4;
+  return W * NS * 64 * SPS * BITS + (KW / 32) * 4 * MR * 16 + (KW / G) * MR * 4 + W * 16 * (KW / G) * 4;
 }
 
 // 4 waves per SIMD: two resident workgroups per CU (128 VGPRs)
 // SPS: 32-input steps per ring stage (8: runs of 128 B or more of each row per stage); NS:
-// ring stages (NS - 1 in flight)
-template <int BITS, bool F16, int MR, int G, int SPS, int NS>
-__global__ __launch_bounds__(VQ_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void vqmv_kernel(const uint16_t *__restrict__ x, int M, int K,
+// ring stages (NS - 1 in flight); W: waves per workgroup (16 W rows per tile)
+template <int BITS, bool F16, int MR, int G, int SPS, int NS, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) void vqmv_kernel(const uint16_t *__restrict__ x, int M, int K,
                                                           const uint32_t *__restrict__ w,
                                                           const uint16_t *__restrict__ sc,
                                                           const uint16_t *__restrict__ bi, int N,
@@ -156,7 +153,7 @@ __global__ __launch_bounds__(VQ_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
   constexpr int SPG = G / 32;                        // steps per group
   constexpr float MAG = F16 ? 1024.f : (BITS == 8 ? 0.f : 128.f);
   char *ring = lds;
-  char *xa = ring + VQ_WAVES * NS * SLOT;
+  char *xa = ring + W * NS * SLOT;
   float *xs = (float *)(xa + (KW / 32) * 4 * MR * 16);  // [group][token]
   uint32_t *sbl = (uint32_t *)(xs + GW * MR);           // [row of the workgroup][group]: s | b << 16
 
@@ -166,10 +163,10 @@ __global__ __launch_bounds__(VQ_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
   const int gpr = K / G;
   const int nwin = (K + KW - 1) / KW;
   // workgroup tiles of 128 rows, this workgroup's are blockIdx.x + k gridDim.x
-  const int ntiles = (N + VQ_WAVES * 16 - 1) / (VQ_WAVES * 16);
+  const int ntiles = (N + W * 16 - 1) / (W * 16);
   const int nk = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
   const int nstage_all = K / SIN;  // stages of one tile
-  auto tile_row = [&](int k) { return ((int)blockIdx.x + k * (int)gridDim.x) * (VQ_WAVES * 16) + wave * 16; };
+  auto tile_row = [&](int k) { return ((int)blockIdx.x + k * (int)gridDim.x) * (W * 16) + wave * 16; };
 
   // DMA of LDS position P = 64 i + lane: tile row P / BITS, piece (P % BITS) ^ swz
   int dma_r[NI], dma_off[NI];
@@ -270,7 +267,7 @@ __global__ __launch_bounds__(VQ_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
         if (k || k0) __syncthreads();  // every wave is done with the previous window
         // x in fragment order (position (step, g, m)) and its group sums, one (group, token)
         // per thread: 8-input partial sums added in input order
-        for (int it = tid; it < ngrp * MR; it += VQ_THREADS) {
+        for (int it = tid; it < ngrp * MR; it += 64 * W) {
           const int gi = it / MR, m = it % MR;
           float sum = 0.f;
           constexpr int CB = G / 8 < 8 ? G / 8 : 8;  // chunks loaded together
@@ -397,34 +394,36 @@ int vq_cus() {
   return cus[dev];
 }
 
-template <int BITS, bool F16, int MR, int G, int SPS, int NS>
+template <int BITS, bool F16, int MR, int G, int SPS, int NS, int W = 8>
 hipError_t launch_vq(const uint16_t *x, int M, int K, const uint32_t *w, const uint16_t *sc, const uint16_t *bi,
                      int N, uint16_t *y, hipStream_t s) {
-  constexpr int lds = vq_lds_bytes<BITS, MR, G, SPS, NS>();
+  constexpr int lds = vq_lds_bytes<BITS, MR, G, SPS, NS, W>();
   static bool raised = false;  // > 64 KB of LDS is an opt-in per kernel
-  auto kern = vqmv_kernel<BITS, F16, MR, G, SPS, NS>;
+  auto kern = vqmv_kernel<BITS, F16, MR, G, SPS, NS, W>;
   if (!raised) {
     const hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     raised = true;
   }
   // persistent workgroups: as many as are resident at once (LDS bound), each walks tiles
-  const int rows_blk = VQ_WAVES * 16, ntiles = (N + rows_blk - 1) / rows_blk;
+  const int rows_blk = W * 16, ntiles = (N + rows_blk - 1) / rows_blk;
   const int per_cu = (160 * 1024) / lds > 0 ? (160 * 1024) / lds : 1;
   const int grid = std::min(ntiles, vq_cus() * per_cu);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(VQ_THREADS), lds, s, x, M, K, w, sc, bi, N, y);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * W), lds, s, x, M, K, w, sc, bi, N, y);
   return hipGetLastError();
 }
 
 // Stage shape per window size (measured on the c1 logits head): 8-step stages (128-B or longer
-// runs of each row) where the deeper LDS still leaves two workgroups per CU, or where one
-// per CU is all that fits anyway; 4-step stages with three in the ring for 5..8 tokens.
+// runs of each row) with two in the ring for up to 4 tokens, and for 5..8 tokens of 4-bit codes
+// with 7-wave workgroups (two per CU still fit); three in the ring for 9..16 tokens (one
+// workgroup per CU).
 template <int BITS, bool F16, int MR, int G>
 hipError_t launch_vq_s(const uint16_t *x, int M, int K, const uint32_t *w, const uint16_t *sc, const uint16_t *bi,
                        int N, uint16_t *y, hipStream_t s) {
   constexpr bool wide_ok = BITS != 8;
   if (wide_ok && K % 256 == 0) {
     if (MR == 4) return launch_vq<BITS, F16, MR, G, 8, 2>(x, M, K, w, sc, bi, N, y, s);
+    if (MR == 8 && BITS == 4) return launch_vq<BITS, F16, MR, G, 8, 2, 7>(x, M, K, w, sc, bi, N, y, s);
     if (MR == 16) return launch_vq<BITS, F16, MR, G, 8, 3>(x, M, K, w, sc, bi, N, y, s);
   }
   return launch_vq<BITS, F16, MR, G, 4, 3>(x, M, K, w, sc, bi, N, y, s);
