@@ -106,6 +106,21 @@ def test_random_codes_match_oracle_and_are_token_local(ops, orc, bits, f16, grou
     _check_token_local(ops, x, w, f16, whole)
 
 
+@pytest.mark.parametrize("bits,f16,group,batch,tokens,K,N", [
+    (4, False, 128, 1, 3, 128, 17),   # one ring stage; one group per row (scalar affine staging)
+    (4, True, 64, 2, 2, 384, 1),      # K not a multiple of 256 (4-step stages), a single output row
+    (5, False, 32, 1, 5, 640, 40),    # 20 groups per row (scalar staging), 8-token fragment
+    (8, True, 128, 1, 12, 1152, 33),  # 16-token fragment, 9 groups per row
+])
+def test_edge_geometries_match_oracle_and_are_token_local(ops, orc, bits, f16, group, batch, tokens, K, N):
+    print(f"verify qmv edge bits={bits} f16={f16} g={group} B={batch} T={tokens} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(K + N)
+    x, w = random_inputs(rng, batch, tokens, K, N, bits, group, f16)
+    whole = _host(_project(ops, x, w, f16).projected_activations)
+    _check_oracle(orc, x, w, f16, whole, (bits, f16, group, batch, tokens, K, N))
+    _check_token_local(ops, x, w, f16, whole)
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_small_batch_quantized_matmul_equals_verification(ops, bits):
     """quantized_matmul_affine of each row alone == the verification projection of the window."""
