@@ -603,10 +603,12 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
     // kernel-attached events: router | gate/up (shared gate/up, routing, sort inside) |
     // down (shared down and the combine inside)
-    hipEvent_t kev[6];
+    hipEvent_t kev[8];
     if (clock) {
-      const int st[3] = {0, 3, 4};
-      for (int i = 0; i < 3; ++i) {
+      // router | gate/up | down | routing (its own kernel from kDecodeRouteOnceT tokens)
+      const int st[4] = {0, 3, 4, 1};
+      const int nst = T >= kDecodeRouteOnceT ? 4 : 3;
+      for (int i = 0; i < nst; ++i) {
         clock->used[st[i]] = true;
         kev[2 * i] = clock->ev[2 * st[i]];
         kev[2 * i + 1] = clock->ev[2 * st[i] + 1];

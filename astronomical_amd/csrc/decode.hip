@@ -19,6 +19,7 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <type_traits>
 
 namespace astro {
 
@@ -205,6 +206,27 @@ __device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs
   }
 }
 
+// rows_task over at most 4 tokens at a time: more tokens run as passes of 4 over the same
+// rows (the second reads the codes from L2), which keeps the kernel's registers at the
+// 4-token footprint; each token's sums are the same either way.
+template <int BITS, int MT, int RP, bool SWIGLU, int NC>
+__device__ __forceinline__ void rows_task_q(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb,
+                                            const uint32_t *uw, const uint16_t *us, const uint16_t *ub,
+                                            int64_t w_rs, int64_t sb_rs, int nrows, int nchunks, int group,
+                                            const uint16_t *x, int64_t ldx, const int *xrows, int m, uint16_t *out,
+                                            int64_t ldo, const int *orows) {
+  if constexpr (MT <= 4) {
+    rows_task<BITS, MT, RP, SWIGLU, NC>(gw, gs, gb, uw, us, ub, w_rs, sb_rs, nrows, nchunks, group, x, ldx, xrows,
+                                        m, out, ldo, orows);
+  } else {
+    for (int t0 = 0; t0 < MT; t0 += 4) {
+      if (t0 >= m) break;
+      rows_task<BITS, 4, RP, SWIGLU, NC>(gw, gs, gb, uw, us, ub, w_rs, sb_rs, nrows, nchunks, group, x, ldx,
+                                         xrows + t0, m - t0 < 4 ? m - t0 : 4, out, ldo, orows + t0);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- D1: router
 
 // Router GEMV: one wave per expert row (bf16 weights), every token.  STEP (the decoder step):
@@ -294,64 +316,17 @@ __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) 
 
 // ---------------------------------------------------------------- D2: route + gate/up
 
-// Workgroups (x, 0): the shared expert, which needs no routing — x < shared_pair_blocks
-// computes 4 (gate row, up row) pairs with the SwiGLU epilogue, x == shared_pair_blocks
-// the output gate z.  Workgroups (x, g + 1): every one recomputes the routing of the <= 8
-// tokens from the logits (route_token), the stable sort of the <= 64 assignments and the
-// table of distinct experts — a few microseconds of one wave's work that saves a dependent
-// kernel boundary — and workgroup (0, 1) publishes them; then it computes rows 4x.. of the
-// gate/up GEMV of the g-th distinct expert for every token routed to it (SwiGLU epilogue).
-template <int BITS, int MT, int NC, int PER>
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
+// Routing of the <= 8 tokens from their logits (route_token), the stable sort of the <= 64
+// assignments and the table of distinct experts, into LDS; with publish, also written to the
+// workspace for the later kernels (ids, scores, sort, inverse, offsets, the table).
+template <int MT, int PER>
+__device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, uint32_t *idx_sh, uint32_t *so_sh,
+                                             uint32_t *sid_sh, uint32_t *key_sh, uint32_t (*route_sh)[kDecodeMaxK],
+                                             uint16_t *sc_sh, uint32_t *g_expert_sh, uint32_t *g_start_sh,
+                                             uint32_t *g_count_sh, uint32_t &ng_sh) {
   constexpr int KM = kDecodeMaxK, AMAX = MT * KM;
-  __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
-  __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
-  __shared__ __attribute__((aligned(16))) uint32_t route_sh[4][KM];
-  __shared__ uint16_t sc_sh[64];
-  __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
-  __shared__ int rows_sh[MT], orows_sh[MT];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-  const int nchunks = p.H / 32;
-  if (blockIdx.y == 0) {
-    if (threadIdx.x < MT) {
-      const int t = threadIdx.x < p.T ? threadIdx.x : p.T - 1;
-      rows_sh[threadIdx.x] = t;
-      orows_sh[threadIdx.x] = p.A + t;
-    }
-    __syncthreads();
-    const int sb = blockIdx.x;
-    if (sb < p.shared_pair_blocks) {
-      const int r0 = (sb * 4 + wave) * kRowsPerWave;
-      if (r0 >= p.Is) return;
-      const int nrows = min(kRowsPerWave, p.Is - r0);
-      if (p.sg_bits == 4)
-        rows_task<4, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
-                                                 p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
-                                                 p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
-                                                 p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
-                                                 p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
-                                                 orows_sh);
-      else
-        rows_task<8, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
-                                                 p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
-                                                 p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
-                                                 p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
-                                                 p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
-                                                 orows_sh);
-      return;
-    }
-    if (sb != p.shared_pair_blocks || wave != 0 || !p.sz_w) return;
-    if (p.sz_bits == 4)
-      rows_task<4, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
-                                     nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
-    else
-      rows_task<8, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
-                                     nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
-    return;
-  }
-  if ((int)blockIdx.x * 4 * kRowsPerWave >= p.I) return;
   const int A = p.A;
-  const bool publish = blockIdx.x == 0 && blockIdx.y == 1;
   for (int t = wave; t < p.T; t += 4) {
     uint32_t my_idx, my_score;
     route_token<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, route_sh[wave],
@@ -419,14 +394,107 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
       p.offsets[e] = e <= p.E ? c : (uint32_t)A;
     }
   }
-  const int g = blockIdx.y - 1;
-  if (g >= (int)ng_sh) return;
-  const uint32_t e = g_expert_sh[g], start = g_start_sh[g], m = g_count_sh[g];
-  if (m > (uint32_t)MT) return;  // a token selects an expert at most once: m <= T <= MT
-  if (threadIdx.x < MT) {
-    const uint32_t i = threadIdx.x < m ? threadIdx.x : m - 1;
-    rows_sh[threadIdx.x] = (int)(so_sh[start + i] / (uint32_t)p.k);
-    orows_sh[threadIdx.x] = (int)(start + i);
+}
+
+// Routing once for a batch of tokens (T >= kDecodeRouteOnceT): one workgroup runs decode_route
+// and publishes it; the gate/up kernel's routed workgroups then read the table instead of
+// each recomputing every token's routing.
+template <int MT, int PER>
+__global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
+  constexpr int KM = kDecodeMaxK;
+  __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
+  __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
+  __shared__ __attribute__((aligned(16))) uint32_t route_sh[4][KM];
+  __shared__ uint16_t sc_sh[64];
+  __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
+  decode_route<MT, PER>(p, true, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh,
+                        g_count_sh, ng_sh);
+}
+
+// Workgroups (x, 0): the shared expert, which needs no routing — x < shared_pair_blocks
+// computes 4 (gate row, up row) pairs with the SwiGLU epilogue, x == shared_pair_blocks
+// the output gate z.  Workgroups (x, g + 1): every one recomputes the routing of the <= 8
+// tokens from the logits (route_token), the stable sort of the <= 64 assignments and the
+// table of distinct experts — a few microseconds of one wave's work that saves a dependent
+// kernel boundary — and workgroup (0, 1) publishes them; then it computes rows 4x.. of the
+// gate/up GEMV of the g-th distinct expert for every token routed to it (SwiGLU epilogue).
+// PRE: the routing was published by decode_route_kernel (read it; do not recompute)
+template <int BITS, int MT, int NC, int PER, bool PRE>
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
+  constexpr int KM = kDecodeMaxK;
+  __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
+  __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
+  __shared__ __attribute__((aligned(16))) uint32_t route_sh[4][KM];
+  __shared__ uint16_t sc_sh[64];
+  __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
+  __shared__ int rows_sh[MT], orows_sh[MT];
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int nchunks = p.H / 32;
+  if (blockIdx.y == 0) {
+    if (threadIdx.x < MT) {
+      const int t = threadIdx.x < p.T ? threadIdx.x : p.T - 1;
+      rows_sh[threadIdx.x] = t;
+      orows_sh[threadIdx.x] = p.A + t;
+    }
+    __syncthreads();
+    const int sb = blockIdx.x;
+    if (sb < p.shared_pair_blocks) {
+      const int r0 = (sb * 4 + wave) * kRowsPerWave;
+      if (r0 >= p.Is) return;
+      const int nrows = min(kRowsPerWave, p.Is - r0);
+      if (p.sg_bits == 4)
+        rows_task_q<4, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
+                                                 p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
+                                                 p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
+                                                 p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
+                                                 p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
+                                                 orows_sh);
+      else
+        rows_task_q<8, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
+                                                 p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
+                                                 p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
+                                                 p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
+                                                 p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
+                                                 orows_sh);
+      return;
+    }
+    if (sb != p.shared_pair_blocks || wave != 0 || !p.sz_w) return;
+    if (p.sz_bits == 4)
+      rows_task_q<4, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
+                                     nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
+    else
+      rows_task_q<8, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
+                                     nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
+    return;
+  }
+  if ((int)blockIdx.x * 4 * kRowsPerWave >= p.I) return;
+  uint32_t e, start, m;
+  if (PRE) {
+    const int g = blockIdx.y - 1;
+    if (g >= (int)*p.n_groups) return;
+    e = p.g_expert[g];
+    start = p.g_start[g];
+    m = p.g_count[g];
+    if (m > (uint32_t)MT) return;  // a token selects an expert at most once: m <= T <= MT
+    if (threadIdx.x < MT) {
+      const uint32_t i = threadIdx.x < m ? threadIdx.x : m - 1;
+      rows_sh[threadIdx.x] = (int)(p.sorted_order[start + i] / (uint32_t)p.k);
+      orows_sh[threadIdx.x] = (int)(start + i);
+    }
+  } else {
+    decode_route<MT, PER>(p, blockIdx.x == 0 && blockIdx.y == 1, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh,
+                          g_expert_sh, g_start_sh, g_count_sh, ng_sh);
+    const int g = blockIdx.y - 1;
+    if (g >= (int)ng_sh) return;
+    e = g_expert_sh[g];
+    start = g_start_sh[g];
+    m = g_count_sh[g];
+    if (m > (uint32_t)MT) return;  // a token selects an expert at most once: m <= T <= MT
+    if (threadIdx.x < MT) {
+      const uint32_t i = threadIdx.x < m ? threadIdx.x : m - 1;
+      rows_sh[threadIdx.x] = (int)(so_sh[start + i] / (uint32_t)p.k);
+      orows_sh[threadIdx.x] = (int)(start + i);
+    }
   }
   __syncthreads();
   const int r0 = (blockIdx.x * 4 + wave) * kRowsPerWave;
@@ -434,10 +502,19 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
   const int nrows = min(kRowsPerWave, p.I - r0);
   const int64_t wo = (int64_t)e * p.gu_w_es + (int64_t)r0 * p.gu_w_rs;
   const int64_t so = (int64_t)e * p.gu_sb_es + (int64_t)r0 * p.gu_sb_rs;
-  rows_task<BITS, MT, kRowsPerWave, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so,
-                                              p.up_w + wo, p.up_s + so, p.up_b + so, p.gu_w_rs,
-                                              p.gu_sb_rs, nrows, nchunks, p.gu_group, p.x, p.H,
-                                              rows_sh, (int)m, p.act + r0, p.act_ld, orows_sh);
+  // the expert's m <= MT tokens: the smallest token count instantiated that covers them (each
+  // token's sums do not depend on it)
+  auto routed_rows = [&](auto mt_tag) {
+    constexpr int M2 = decltype(mt_tag)::value;
+    rows_task_q<BITS, M2, kRowsPerWave, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
+                                                p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows, nchunks,
+                                                p.gu_group, p.x, p.H, rows_sh, (int)m, p.act + r0, p.act_ld,
+                                                orows_sh);
+  };
+  if (m <= 1) routed_rows(std::integral_constant<int, 1>());
+  else if (MT > 2 && m <= 2) routed_rows(std::integral_constant<int, (MT > 2 ? 2 : MT)>());
+  else if (MT > 4 && m <= 4) routed_rows(std::integral_constant<int, (MT > 4 ? 4 : MT)>());
+  else routed_rows(std::integral_constant<int, MT>());
 }
 
 // ---------------------------------------------------------------- D3: down + combine
@@ -565,8 +642,21 @@ void launch_gate_up_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev
   // x: routed row blocks, or the shared expert's pair blocks and its output-gate block
   const int routed_x = (a.I + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave);
   const int shared_x = a.Is > 0 ? a.shared_pair_blocks + 1 : 0;
-  launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER>, dim3(std::max(routed_x, shared_x), a.max_groups + 1),
-               s, ev, a);
+  const dim3 grid(std::max(routed_x, shared_x), a.max_groups + 1);
+  if (a.T >= kDecodeRouteOnceT)
+    launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, true>, grid, s, ev, a);
+  else
+    launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, false>, grid, s, ev, a);
+}
+
+template <int MT>
+void launch_route_mt(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
+  const int per = (a.E + 63) / 64;
+  if (per <= 1) launch_timed(decode_route_kernel<MT, 1>, dim3(1), s, ev, a);
+  else if (per <= 2) launch_timed(decode_route_kernel<MT, 2>, dim3(1), s, ev, a);
+  else if (per <= 4) launch_timed(decode_route_kernel<MT, 4>, dim3(1), s, ev, a);
+  else if (per <= 8) launch_timed(decode_route_kernel<MT, 8>, dim3(1), s, ev, a);
+  else launch_timed(decode_route_kernel<MT, 16>, dim3(1), s, ev, a);
 }
 
 template <int BITS, int MT, int NC>
@@ -654,7 +744,16 @@ hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, const hipEven
   else launch_router<8>(a, a.router_blocks, s, e1);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // D2: shared gate/up, routing, routed gate/up
+  // routing once for a batch of tokens (kev[6..7], when given, time it)
+  if (a.T >= kDecodeRouteOnceT) {
+    const hipEvent_t *er = kev ? kev + 6 : nullptr;
+    if (mt == 2) launch_route_mt<2>(a, s, er);
+    else if (mt == 4) launch_route_mt<4>(a, s, er);
+    else launch_route_mt<8>(a, s, er);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  // D2: shared gate/up, routing (T = 1), routed gate/up
   if (a.gu_bits == 8) launch_gate_up<8>(a, mt, s, e2);
   else launch_gate_up<4>(a, mt, s, e2);
   e = hipGetLastError();

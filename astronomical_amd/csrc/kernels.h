@@ -151,9 +151,13 @@ constexpr int kDecodeStepLds = 60 * 1024;
 
 bool decode_supported(const DecodeArgs &a);
 constexpr int kDecodeRowsPerWave = 1;  // must match kRowsPerWave in decode.hip
+// from this many tokens a one-workgroup kernel routes the batch once, instead of every routed
+// gate/up workgroup recomputing every token's routing
+constexpr int kDecodeRouteOnceT = 2;
 constexpr int kDecodeMaxK = 8;         // experts per token the decode combine unrolls
-// launches the three decode kernels (router | shared gate/up + routing + routed gate/up |
-// down + combine); kev (nullable) = start/stop event pairs recorded around each kernel
+// launches the decode kernels (router | [routing, T >= kDecodeRouteOnceT] | shared gate/up +
+// routing (T = 1) + routed gate/up | down + combine); kev (nullable) = start/stop event pairs
+// recorded around the router, gate/up and down kernels, and (kev[6..7]) the routing kernel
 hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, const hipEvent_t *kev);
 
 }  // namespace astro

@@ -399,6 +399,11 @@ class MoeBlock:
 
     __call__ = forward
 
+    def verification_workspace_bytes(self, tokens: int) -> int:
+        n = C.c_size_t()
+        call("astro_moe_verification_workspace_bytes", C.byref(self._struct), tokens, C.byref(n))
+        return n.value
+
     def target_verification_forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
                                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
         """forward_moe_resident_target_verification (resident_execution.rs:146-208): the block
@@ -407,11 +412,10 @@ class MoeBlock:
         x2 = x.contiguous().view(torch.bfloat16).reshape(-1, self.weights.hidden)
         T = x2.shape[0]
         y = out if out is not None else torch.empty_like(x2)
-        n = C.c_size_t()
-        call("astro_moe_verification_workspace_bytes", C.byref(self._struct), T, C.byref(n))
+        need = self.verification_workspace_bytes(T)
         ws = workspace
-        if ws is None or ws.numel() < n.value:
-            ws = torch.empty(max(n.value, 1), dtype=torch.uint8, device=self.device)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device=self.device)
         call("astro_moe_block_forward_verification", C.byref(self._struct), _ptr(x2), T, _ptr(y), _ptr(ws),
              ws.numel(), _stream(self.device))
         return y

@@ -382,6 +382,42 @@ def verification_qmv(CF, DS, ops, torch, reps=20, vocab=248_320):
         out[f"{bits}bit"] = res
         del w, codes, sc, bi
         torch.cuda.empty_cache()
+    # the MoE block over a verification window (every row bit-equal to its one-token block):
+    # a hipGraph of the window through 40 distinct c1 layers, per-layer time
+    nL = 40
+    layers = [DS.make_layer_device(CF.C1, layer=l) for l in range(nL)]
+    blocks = [ops.MoeBlock(L) for L in layers]
+    blk_res = {}
+    for T in (2, 4, 8):
+        xs = DS.make_tokens_device(CF.C1, nL * T, step=7).reshape(nL, T, H)
+        ys = torch.empty_like(xs)
+        wsz = blocks[0].verification_workspace_bytes(T)
+        ws = torch.empty(wsz, dtype=torch.uint8, device="cuda")
+
+        def window_pass():
+            for l in range(nL):
+                blocks[l].target_verification_forward(xs[l], out=ys[l], workspace=ws)
+        window_pass()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            window_pass()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us_layer = e0.elapsed_time(e1) * 1000 / (5 * nL)
+        blk_res[f"T{T}"] = {"us_per_layer": round(us_layer, 2), "tokens_per_s": round(T / (us_layer * 1e-6), 1)}
+        del g, xs, ys, ws
+    out["block_window"] = {"workload": f"c1 MoE block in verification mode (rows unsorted, token-local), "
+                                       f"a window of T tokens through a graph of {nL} distinct layers",
+                           **blk_res}
+    del layers, blocks
+    torch.cuda.empty_cache()
     log(f"verification qmv: {json.dumps(out)}")
     return out
 
