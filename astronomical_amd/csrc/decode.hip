@@ -327,7 +327,8 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, 
   constexpr int KM = kDecodeMaxK, AMAX = MT * KM;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
   const int A = p.A;
-  for (int t = wave; t < p.T; t += 4) {
+  const int nwaves = (int)(blockDim.x >> 6);
+  for (int t = wave; t < p.T; t += nwaves) {
     uint32_t my_idx, my_score;
     route_token<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, route_sh[wave],
                          my_idx, my_score);
@@ -387,7 +388,7 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, 
   __syncthreads();
   if (publish) {
     // expert offsets [E+2] (E+1: trailing out-of-range bucket, empty here)
-    for (int e = threadIdx.x; e <= p.E + 1; e += 256) {
+    for (int e = threadIdx.x; e <= p.E + 1; e += (int)blockDim.x) {
       uint32_t c = 0;
 #pragma unroll
       for (int i = 0; i < AMAX; ++i) c += (i < A) & (sid_sh[i] < (uint32_t)e);
@@ -400,11 +401,11 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, 
 // and publishes it; the gate/up kernel's routed workgroups then read the table instead of
 // each recomputing every token's routing.
 template <int MT, int PER>
-__global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
+__global__ __launch_bounds__(64 * MT) void decode_route_kernel(const DecodeArgs p) {
   constexpr int KM = kDecodeMaxK;
   __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
   __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
-  __shared__ __attribute__((aligned(16))) uint32_t route_sh[4][KM];
+  __shared__ __attribute__((aligned(16))) uint32_t route_sh[MT][KM];
   __shared__ uint16_t sc_sh[64];
   __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
   decode_route<MT, PER>(p, true, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh,
@@ -418,8 +419,9 @@ __global__ __launch_bounds__(256) void decode_route_kernel(const DecodeArgs p) {
 // table of distinct experts — a few microseconds of one wave's work that saves a dependent
 // kernel boundary — and workgroup (0, 1) publishes them; then it computes rows 4x.. of the
 // gate/up GEMV of the g-th distinct expert for every token routed to it (SwiGLU epilogue).
-// PRE: the routing was published by decode_route_kernel (read it; do not recompute)
-template <int BITS, int MT, int NC, int PER, bool PRE>
+// PRE: the routing was published by decode_route_kernel (read it; do not recompute).  RPW:
+// (gate, up) row pairs per routed wave (more for larger batches: fewer, fuller workgroups)
+template <int BITS, int MT, int NC, int PER, bool PRE, int RPW>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
   constexpr int KM = kDecodeMaxK;
   __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
@@ -467,7 +469,7 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
                                      nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
     return;
   }
-  if ((int)blockIdx.x * 4 * kRowsPerWave >= p.I) return;
+  if ((int)blockIdx.x * 4 * RPW >= p.I) return;
   uint32_t e, start, m;
   if (PRE) {
     const int g = blockIdx.y - 1;
@@ -497,16 +499,16 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
     }
   }
   __syncthreads();
-  const int r0 = (blockIdx.x * 4 + wave) * kRowsPerWave;
+  const int r0 = (blockIdx.x * 4 + wave) * RPW;
   if (r0 >= p.I) return;
-  const int nrows = min(kRowsPerWave, p.I - r0);
+  const int nrows = min(RPW, p.I - r0);
   const int64_t wo = (int64_t)e * p.gu_w_es + (int64_t)r0 * p.gu_w_rs;
   const int64_t so = (int64_t)e * p.gu_sb_es + (int64_t)r0 * p.gu_sb_rs;
   // the expert's m <= MT tokens: the smallest token count instantiated that covers them (each
   // token's sums do not depend on it)
   auto routed_rows = [&](auto mt_tag) {
     constexpr int M2 = decltype(mt_tag)::value;
-    rows_task_q<BITS, M2, kRowsPerWave, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
+    rows_task_q<BITS, M2, RPW, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
                                                 p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows, nchunks,
                                                 p.gu_group, p.x, p.H, rows_sh, (int)m, p.act + r0, p.act_ld,
                                                 orows_sh);
@@ -637,26 +639,46 @@ void launch_timed(Kernel kernel, dim3 grid, hipStream_t s, const hipEvent_t *ev,
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, a);
 }
 
-template <int BITS, int MT, int NC, int PER>
-void launch_gate_up_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
+template <int BITS, int MT, int NC, int PER, int RPW>
+void launch_gate_up_rpw(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   // x: routed row blocks, or the shared expert's pair blocks and its output-gate block
-  const int routed_x = (a.I + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave);
+  const int routed_x = (a.I + 4 * RPW - 1) / (4 * RPW);
   const int shared_x = a.Is > 0 ? a.shared_pair_blocks + 1 : 0;
   const dim3 grid(std::max(routed_x, shared_x), a.max_groups + 1);
   if (a.T >= kDecodeRouteOnceT)
-    launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, true>, grid, s, ev, a);
+    launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, true, RPW>, grid, s, ev, a);
   else
-    launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, false>, grid, s, ev, a);
+    launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, false, RPW>, grid, s, ev, a);
+}
+
+template <int BITS, int MT, int NC, int PER>
+void launch_gate_up_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
+  // one row pair per routed wave for a single token (the chip has wave slots to spare); a
+  // batch selects up to 8x more distinct experts, so each wave takes more rows
+  if (MT <= 1) launch_gate_up_rpw<BITS, MT, NC, PER, kRowsPerWave>(a, s, ev);
+  else if (MT <= 2) launch_gate_up_rpw<BITS, MT, NC, PER, 2>(a, s, ev);
+  else launch_gate_up_rpw<BITS, MT, NC, PER, 4>(a, s, ev);
+}
+
+// one workgroup, one wave per token slot (at least 4 waves: the offsets loop and wave 0's sort
+// are sized for a 256-thread block or more)
+template <int MT, int PER>
+void launch_route_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
+  constexpr int W = MT > 4 ? MT : 4;
+  if (ev)
+    hipExtLaunchKernelGGL((decode_route_kernel<W, PER>), dim3(1), dim3(64 * W), 0, s, ev[0], ev[1], 0, a);
+  else
+    hipLaunchKernelGGL((decode_route_kernel<W, PER>), dim3(1), dim3(64 * W), 0, s, a);
 }
 
 template <int MT>
 void launch_route_mt(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   const int per = (a.E + 63) / 64;
-  if (per <= 1) launch_timed(decode_route_kernel<MT, 1>, dim3(1), s, ev, a);
-  else if (per <= 2) launch_timed(decode_route_kernel<MT, 2>, dim3(1), s, ev, a);
-  else if (per <= 4) launch_timed(decode_route_kernel<MT, 4>, dim3(1), s, ev, a);
-  else if (per <= 8) launch_timed(decode_route_kernel<MT, 8>, dim3(1), s, ev, a);
-  else launch_timed(decode_route_kernel<MT, 16>, dim3(1), s, ev, a);
+  if (per <= 1) launch_route_per<MT, 1>(a, s, ev);
+  else if (per <= 2) launch_route_per<MT, 2>(a, s, ev);
+  else if (per <= 4) launch_route_per<MT, 4>(a, s, ev);
+  else if (per <= 8) launch_route_per<MT, 8>(a, s, ev);
+  else launch_route_per<MT, 16>(a, s, ev);
 }
 
 template <int BITS, int MT, int NC>

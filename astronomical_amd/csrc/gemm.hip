@@ -582,7 +582,9 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
 #pragma unroll
     for (int f = 0; f < 4; ++f) acc[rb][f] = f32x4{0.f, 0.f, 0.f, 0.f};
   ring_barrier();  // step 0's A and weights are ready
-  const bool small = m_valid <= 64;
+  // row-block pairs the tile needs: 64, 96 or 128 rows (about half of the experts of a
+  // uniform 2048-token prefill hold 65-96 rows, which then skip a quarter of the MFMAs)
+  const int nbu = m_valid <= 64 ? 2 : m_valid <= 96 ? 3 : 4;
   auto consume = [&](auto nb_tag) {
     constexpr int NB = decltype(nb_tag)::value;
     for (int k = 0; k < nk; ++k) {
@@ -592,14 +594,15 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
       ring_barrier();
     }
   };
-  if (small) consume(std::integral_constant<int, 2>());
+  if (nbu == 2) consume(std::integral_constant<int, 2>());
+  else if (nbu == 3) consume(std::integral_constant<int, 3>());
   else consume(std::integral_constant<int, 4>());
 
   // ---- epilogue: lane holds column (lane & 15) of each block, rows 4 (lane >> 4) + i
   const int c16 = lane & 15, kq = lane >> 4;
 #pragma unroll
   for (int rb = 0; rb < 8; ++rb) {
-    if (small && rb >= 4) break;
+    if (rb >= 2 * nbu) break;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = rb * 16 + kq * 4 + i;

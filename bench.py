@@ -204,6 +204,7 @@ def main():
     extra = None
     if not args.no_extra:
         extra = decoder_step(CF, DS, ops, torch, blocks, K, W)
+        extra["c1_decode_batched"] = batched_decode(CF, DS, ops, torch, blocks, K, W)
         extra.update(other_configs(CF, DS, ops, torch, K, W, layers[0]))
         extra["verification_lm_head"] = verification_qmv(CF, DS, ops, torch)
 
@@ -419,6 +420,51 @@ def verification_qmv(CF, DS, ops, torch, reps=20, vocab=248_320):
     del layers, blocks
     torch.cuda.empty_cache()
     log(f"verification qmv: {json.dumps(out)}")
+    return out
+
+
+def batched_decode(CF, DS, ops, torch, blocks, K, W, sizes=(2, 4, 8)):
+    """c1 decode at B = 2, 4, 8 tokens per step (production mode: the sorted combine at 64
+    assignments) through a graph of all the layers, as the B = 1 headline.  Credited bytes per
+    layer = (distinct routed experts of the step + the shared expert) x page bytes, the
+    distinct experts counted from each layer's routing of the step's tokens."""
+    import numpy as np
+    cfg = CF.C1
+    H, nL, dev = cfg.hidden, len(blocks), torch.device("cuda")
+    out = {"workload": f"c1 decode, B tokens per step through a graph of {nL} distinct layers"}
+    for B in sizes:
+        x = DS.make_tokens_device(cfg, nL * B, step=11).reshape(nL, B, H)
+        y = torch.empty_like(x)
+        ws = torch.empty(blocks[0].workspace_bytes(B), dtype=torch.uint8, device=dev)
+        distinct = []
+        for l in range(nL):
+            blocks[l].forward(x[l], out=y[l], workspace=ws)
+            distinct.append(len(np.unique(blocks[l].trace(B, workspace=ws)["indices"])))
+
+        def step():
+            for l in range(nL):
+                blocks[l].forward(x[l], out=y[l], workspace=ws)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        for _ in range(W):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(K):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / K / nL * 1000
+        u = float(np.mean(distinct))
+        credited = (u + 1) * cfg.page_bytes
+        gbs = credited / (us * 1e-6) / 1e9
+        out[f"B{B}"] = {"us_per_layer": round(us, 2), "tokens_per_s": round(B / (us * 1e-6), 1),
+                        "distinct_experts": round(u, 2), "credited_bytes_per_layer": int(credited),
+                        "achieved_GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        del g, x, y, ws
+    log(f"batched decode: {json.dumps(out)}")
     return out
 
 
