@@ -414,13 +414,14 @@ __global__ __launch_bounds__(64 * MT) void decode_route_kernel(const DecodeArgs 
 
 // Workgroups (x, 0): the shared expert, which needs no routing — x < shared_pair_blocks
 // computes 4 (gate row, up row) pairs with the SwiGLU epilogue, x == shared_pair_blocks
-// the output gate z.  Workgroups (x, g + 1): every one recomputes the routing of the <= 8
-// tokens from the logits (route_token), the stable sort of the <= 64 assignments and the
-// table of distinct experts — a few microseconds of one wave's work that saves a dependent
-// kernel boundary — and workgroup (0, 1) publishes them; then it computes rows 4x.. of the
-// gate/up GEMV of the g-th distinct expert for every token routed to it (SwiGLU epilogue).
-// PRE: the routing was published by decode_route_kernel (read it; do not recompute).  RPW:
-// (gate, up) row pairs per routed wave (more for larger batches: fewer, fuller workgroups)
+// the output gate z.  Workgroups (x, g + 1): rows of the gate/up GEMV of the g-th distinct
+// expert for every token routed to it (SwiGLU epilogue).  Without PRE (one token) every one
+// of them first recomputes the routing from the logits (route_token), the stable sort of the
+// assignments and the table of distinct experts — a few microseconds of one wave's work that
+// saves a dependent kernel boundary — and workgroup (0, 1) publishes them.  With PRE (batches
+// from kDecodeRouteOnceT tokens) decode_route_kernel has published the routing and the
+// workgroups read it instead.  RPW: (gate, up) row pairs per routed wave (more for larger
+// batches: fewer, fuller workgroups).
 template <int BITS, int MT, int NC, int PER, bool PRE, int RPW>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
   constexpr int KM = kDecodeMaxK;
@@ -660,8 +661,8 @@ void launch_gate_up_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev
   else launch_gate_up_rpw<BITS, MT, NC, PER, 4>(a, s, ev);
 }
 
-// one workgroup, one wave per token slot (at least 4 waves: the offsets loop and wave 0's sort
-// are sized for a 256-thread block or more)
+// one workgroup, one wave per token slot and at least 4 (the E + 2 expert offsets are spread
+// over every thread of the block)
 template <int MT, int PER>
 void launch_route_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   constexpr int W = MT > 4 ? MT : 4;
