@@ -36,28 +36,30 @@ __device__ __forceinline__ uint32_t pack_bf2_hw(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Raw loads of one K step's weights: codes (or dense bf16) and the group's scale and bias as
+// bf16 bits.  The bits are widened to float only when the step is dequantised, so nothing
+// waits for these loads when they are issued.
 struct BRegs {
   u32x4 q[4];
-  float s, b;
+  uint32_t s, b;
 };
 
 template <int KIND>
 __device__ __forceinline__ void load_b(BRegs &r, const uint32_t *wrow, const uint16_t *srow,
                                        const uint16_t *brow, const uint16_t *drow, int k0,
-                                       int half, int group, bool valid) {
-  if (!valid) return;
+                                       int half, int group) {
   if (KIND == kBQ4) {
     r.q[0] = *(const u32x4 *)(wrow + (k0 >> 3) + half * 4);
     const int g = (k0 + 32 * half) / group;
-    r.s = bf2f(srow[g]);
-    r.b = bf2f(brow[g]);
+    r.s = srow[g];
+    r.b = brow[g];
   } else if (KIND == kBQ8) {
     const u32x4 *p = (const u32x4 *)(wrow + (k0 >> 2) + half * 8);
     r.q[0] = p[0];
     r.q[1] = p[1];
     const int g = (k0 + 32 * half) / group;
-    r.s = bf2f(srow[g]);
-    r.b = bf2f(brow[g]);
+    r.s = srow[g];
+    r.b = brow[g];
   } else {
     const u32x4 *p = (const u32x4 *)(drow + k0 + half * 32);
     r.q[0] = p[0];
@@ -74,6 +76,7 @@ __device__ __forceinline__ void store_b(uint16_t *dst, const BRegs &r, bool vali
   if (!valid) {
     for (int i = 0; i < 4; ++i) out[i] = u32x4{0, 0, 0, 0};
   } else if (KIND == kBQ4) {
+    const float sc = bf2f(r.s), bi = bf2f(r.b);
 #pragma unroll
     for (int wi = 0; wi < 4; ++wi) {
       const uint32_t w = r.q[0][wi];
@@ -82,18 +85,19 @@ __device__ __forceinline__ void store_b(uint16_t *dst, const BRegs &r, bool vali
       for (int j = 0; j < 4; ++j) {
         const float q0 = (float)((w >> (8 * j)) & 15u);
         const float q1 = (float)((w >> (8 * j + 4)) & 15u);
-        p[j] = pack_bf2_hw(__builtin_fmaf(r.s, q0, r.b), __builtin_fmaf(r.s, q1, r.b));
+        p[j] = pack_bf2_hw(__builtin_fmaf(sc, q0, bi), __builtin_fmaf(sc, q1, bi));
       }
       out[wi] = u32x4{p[0], p[1], p[2], p[3]};
     }
   } else if (KIND == kBQ8) {
+    const float sc = bf2f(r.s), bi = bf2f(r.b);
 #pragma unroll
     for (int wi = 0; wi < 8; ++wi) {
       const uint32_t w = r.q[wi >> 2][wi & 3];
       const float q0 = (float)(w & 255u), q1 = (float)((w >> 8) & 255u);
       const float q2 = (float)((w >> 16) & 255u), q3 = (float)(w >> 24);
-      const uint32_t p0 = pack_bf2_hw(__builtin_fmaf(r.s, q0, r.b), __builtin_fmaf(r.s, q1, r.b));
-      const uint32_t p1 = pack_bf2_hw(__builtin_fmaf(r.s, q2, r.b), __builtin_fmaf(r.s, q3, r.b));
+      const uint32_t p0 = pack_bf2_hw(__builtin_fmaf(sc, q0, bi), __builtin_fmaf(sc, q1, bi));
+      const uint32_t p1 = pack_bf2_hw(__builtin_fmaf(sc, q2, bi), __builtin_fmaf(sc, q3, bi));
       out[wi >> 1][(wi & 1) * 2] = p0;
       out[wi >> 1][(wi & 1) * 2 + 1] = p1;
     }
@@ -166,18 +170,20 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
   } else {
     n = ntile * BR + br;
   }
+  // Every load of the K loop is unconditional, so the compiler can count the loads in flight
+  // and wait for exactly the stage it needs: rows past N load row N - 1 (and store zeros),
+  // rows past m_valid load the tile's first row (their products are never stored).
   const bool bvalid = n < p.N;
+  const int nl = bvalid ? n : p.N - 1;
   const uint32_t *wrow = nullptr;
   const uint16_t *srow = nullptr, *brow = nullptr, *drow = nullptr;
-  if (bvalid) {
-    if (KIND == kBDense) {
-      drow = p.bd + (int64_t)n * p.bd_row_stride;
-    } else {
-      wrow = (upper ? p.w1 : p.w0) + (int64_t)expert * p.w_expert_stride + (int64_t)n * p.w_row_stride;
-      const int64_t so = (int64_t)expert * p.sb_expert_stride + (int64_t)n * p.sb_row_stride;
-      srow = (upper ? p.s1 : p.s0) + so;
-      brow = (upper ? p.b1 : p.b0) + so;
-    }
+  if (KIND == kBDense) {
+    drow = p.bd + (int64_t)nl * p.bd_row_stride;
+  } else {
+    wrow = (upper ? p.w1 : p.w0) + (int64_t)expert * p.w_expert_stride + (int64_t)nl * p.w_row_stride;
+    const int64_t so = (int64_t)expert * p.sb_expert_stride + (int64_t)nl * p.sb_row_stride;
+    srow = (upper ? p.s1 : p.s0) + so;
+    brow = (upper ? p.b1 : p.b0) + so;
   }
 
   // ---- per-thread activation rows (load stage): 4 chunks of 16 B
@@ -186,13 +192,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = (tid >> 3) + 32 * i;
-    arow[i] = nullptr;
-    if (r < m_valid) {
-      const int gr = row0 + r;
-      int src = p.a_rows ? (int)(p.a_rows[gr] / (uint32_t)p.a_div) : gr;
-      if (p.a_rows2) src = (int)p.a_rows2[src];
-      arow[i] = p.A + (int64_t)src * p.lda + acol;
-    }
+    const int gr = row0 + (r < m_valid ? r : 0);
+    int src = p.a_rows ? (int)(p.a_rows[gr] / (uint32_t)p.a_div) : gr;
+    if (p.a_rows2) src = (int)p.a_rows2[src];
+    arow[i] = p.A + (int64_t)src * p.lda + acol;
   }
 
   // ---- MFMA ownership
@@ -212,24 +215,24 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
     acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  u32x4 areg[4];
-  BRegs breg;
-  auto load_stage = [&](int k0) {
+  // two register stages: the loads of step k + 2 are issued while step k computes, so each
+  // step has a step's worth of time more for its memory round trip
+  u32x4 areg[2][4];
+  BRegs breg[2];
+  auto load_stage = [&](int k0, int b) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      areg[i] = arow[i] ? *(const u32x4 *)(arow[i] + k0) : u32x4{0, 0, 0, 0};
-    load_b<KIND>(breg, wrow, srow, brow, drow, k0, half, p.group, bvalid);
+    for (int i = 0; i < 4; ++i) areg[b][i] = *(const u32x4 *)(arow[i] + k0);
+    load_b<KIND>(breg[b], wrow, srow, brow, drow, k0, half, p.group);
   };
-
-  load_stage(0);
-  for (int k0 = 0; k0 < p.K; k0 += BK) {
+  auto step = [&](int k0, int b) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *(u32x4 *)(As + ((tid >> 3) + 32 * i) * LDSP + acol) = areg[i];
-    store_b<KIND>(Bs + br * LDSP + 32 * half, breg, bvalid);
+      *(u32x4 *)(As + ((tid >> 3) + 32 * i) * LDSP + acol) = areg[b][i];
+    store_b<KIND>(Bs + br * LDSP + 32 * half, breg[b], bvalid);
     __syncthreads();
-    if (k0 + BK < p.K) load_stage(k0 + BK);
+    // past the last step the stage reloads the last step (never stored)
+    load_stage(min(k0 + 2 * BK, p.K - BK), b);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int koff = kk * 32 + (lane >> 4) * 8;
@@ -244,7 +247,17 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
         }
       }
     }
+  };
+
+  load_stage(0, 0);
+  load_stage(min(BK, p.K - BK), 1);
+  int k0 = 0;
+  for (; k0 + 2 * BK <= p.K; k0 += 2 * BK) {
+    step(k0, 0);
+    step(k0 + BK, 1);
   }
+  if (k0 < p.K) step(k0, 0);  // an odd number of K steps
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // the trailing reloads land before the workgroup ends
 
   // ---- epilogue: lane holds column (lane & 15), rows 4*(lane >> 4) + i of each block
 #pragma unroll
