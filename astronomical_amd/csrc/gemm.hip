@@ -226,9 +226,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
   };
   auto step = [&](int k0, int b) {
     __syncthreads();
+    // only the row blocks the MFMAs read (small tiles skip most of the tile's LDS writes)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *(u32x4 *)(As + ((tid >> 3) + 32 * i) * LDSP + acol) = areg[b][i];
+      if ((tid >> 3) + 32 * i < nrb * 16) *(u32x4 *)(As + ((tid >> 3) + 32 * i) * LDSP + acol) = areg[b][i];
     store_b<KIND>(Bs + br * LDSP + 32 * half, breg[b], bvalid);
     __syncthreads();
     // past the last step the stage reloads the last step (never stored)
