@@ -175,6 +175,25 @@ def test_gather_qmm_matches_oracle(ops, orc, bits, group, sorted_ids):
     assert_bf16_close(got, want, f"gather_qmm {bits}-bit g{group}")
 
 
+@pytest.mark.parametrize("bits,group", [(4, 32), (4, 64), (8, 32), (8, 64)])
+@pytest.mark.parametrize("K", [64, 576])
+def test_gather_qmm_odd_and_single_k_steps(ops, orc, bits, group, K):
+    """The 4-wave grouped GEMM's two load stages over one K step (K = 64) and an odd number of
+    steps (K = 576, a tail step after the pairs), with a partial last column tile (N = 130) and
+    experts of 1-70 rows."""
+    rng = np.random.default_rng(bits * 1000 + group + K)
+    E, N, rows = 5, 130, 160
+    aff = _random_affine(rng, E, N, K, bits, group)
+    x = f32_to_bf16(rng.standard_normal((rows, K)).astype(np.float32))
+    ids = np.sort(np.concatenate([np.full(70, 1), np.full(1, 2), rng.integers(0, E, size=rows - 71)]))
+    ids = ids.astype(np.uint32)
+    want = orc.gather_qmm(x, aff, ids)
+    daff = aff.map(lambda a: _dev_u32(a) if a.dtype == np.uint32 else _dev_bf16(a))
+    got = _np(ops.gather_expert_projection(_dev_bf16(x), daff, _dev_u32(ids),
+                                           ops.ExpertAssignmentOrder.SORTED_BY_EXPERT))
+    assert_bf16_close(got, want, f"gather_qmm {bits}-bit g{group} K{K}")
+
+
 # ------------------------------------------------------------------ elementwise stages
 
 def test_swiglu_bit_exact(ops, orc):
