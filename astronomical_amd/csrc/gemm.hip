@@ -264,12 +264,19 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
 #pragma unroll
   for (int rb = 0; rb < 8; ++rb) {
     if (rb >= nrb) continue;
+    // the block's four scattered destination rows, loaded together (one round trip)
+    int dsts[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb * 16 + (lane >> 4) * 4 + i;
+      const int gr = row0 + (r < m_valid ? r : 0);
+      dsts[i] = p.c_rows ? (int)p.c_rows[gr] : gr;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = rb * 16 + (lane >> 4) * 4 + i;
       if (r >= m_valid) continue;
-      const int gr = row0 + r;
-      const int dst = p.c_rows ? (int)p.c_rows[gr] : gr;
+      const int dst = dsts[i];
       uint16_t *crow = p.C + (int64_t)dst * p.ldc;
       if (EPI == kEpiSwiglu) {
         const int col = ntile * 64 + wave * 16 + (lane & 15);
@@ -348,26 +355,11 @@ __device__ __forceinline__ void wait_vmcnt_le(int n) {
   }
 }
 
-// 8 codes of one word (4-bit: 8 nibbles, LSB first) -> 8 bf16 in input order.  The
-// nibble masks go through asm so that the compiler keeps them as one AND each and converts
-// every byte with one v_cvt_f32_ubyte{0..3} (it would otherwise re-derive each nibble
-// with a bit-field extract first).
-__device__ __forceinline__ u32x4 dequant8_q4(uint32_t w, float s, float b) {
-  uint32_t lo, hi;
-  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
-  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi) : "v"(w >> 4));
-  u32x4 o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float q0 = (float)((lo >> (8 * i)) & 255u), q1 = (float)((hi >> (8 * i)) & 255u);
-    o[i] = pack_bf2_hw(__builtin_fmaf(s, q0, b), __builtin_fmaf(s, q1, b));
-  }
-  return o;
-}
-
-// 4 words of codes (32 inputs) -> 4 chunks of 8 bf16, the words' conversions interleaved
-// (each byte position converts 8 independent values) so that dependent instructions are
-// several issues apart.
+// 4 words of codes (32 inputs, 4-bit, LSB first) -> 4 chunks of 8 bf16, the words'
+// conversions interleaved (each byte position converts 8 independent values) so that
+// dependent instructions are several issues apart.  The nibble masks go through asm so that
+// the compiler keeps them as one AND each and converts every byte with one
+// v_cvt_f32_ubyte{0..3} (it would otherwise re-derive each nibble with a bit-field extract).
 __device__ __forceinline__ void dequant32_q4(const u32x4 &q, float s, float b, u32x4 (&o)[4]) {
   uint32_t lo[4], hi[4];
 #pragma unroll
@@ -617,12 +609,19 @@ __global__ __launch_bounds__(64 * (WPW + 4)) void ws_gemm_kernel(const GemmArgs 
 #pragma unroll
   for (int rb = 0; rb < 8; ++rb) {
     if (rb >= 2 * nbu) break;
+    // the block's four scattered destination rows, loaded together (one round trip)
+    int dsts[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb * 16 + kq * 4 + i;
+      const int gr = row0 + (r < m_valid ? r : 0);
+      dsts[i] = p.c_rows ? (int)p.c_rows[gr] : gr;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = rb * 16 + kq * 4 + i;
       if (r >= m_valid) continue;
-      const int gr = row0 + r;
-      const int dst = p.c_rows ? (int)p.c_rows[gr] : gr;
+      const int dst = dsts[i];
       uint16_t *crow = p.C + (int64_t)dst * p.ldc;
       if (EPI == kEpiSwiglu) {
 #pragma unroll
