@@ -186,16 +186,42 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
     brow = (upper ? p.b1 : p.b0) + so;
   }
 
+  // two register stages: the loads of step k + 2 are issued while step k computes, so each
+  // step has a step's worth of time more for its memory round trip.  The weights of steps 0
+  // and 1 need only the expert, so they are issued before the activation rows' index loads.
+  u32x4 areg[2][4];
+  BRegs breg[2];
+  const int k1 = min(BK, p.K - BK);
+  load_b<KIND>(breg[0], wrow, srow, brow, drow, 0, half, p.group);
+  load_b<KIND>(breg[1], wrow, srow, brow, drow, k1, half, p.group);
+
   // ---- per-thread activation rows (load stage): 4 chunks of 16 B
   const uint16_t *arow[4];
   const int acol = (tid & 7) * 8;
+  {
+    // each level of row indices in four loads issued together (one round trip per level)
+    int src[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (tid >> 3) + 32 * i;
-    const int gr = row0 + (r < m_valid ? r : 0);
-    int src = p.a_rows ? (int)(p.a_rows[gr] / (uint32_t)p.a_div) : gr;
-    if (p.a_rows2) src = (int)p.a_rows2[src];
-    arow[i] = p.A + (int64_t)src * p.lda + acol;
+    for (int i = 0; i < 4; ++i) {
+      const int r = (tid >> 3) + 32 * i;
+      src[i] = row0 + (r < m_valid ? r : 0);
+    }
+    if (p.a_rows) {
+      uint32_t tt[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tt[i] = p.a_rows[src[i]];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) src[i] = (int)(tt[i] / (uint32_t)p.a_div);
+    }
+    if (p.a_rows2) {
+      uint32_t tt[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tt[i] = p.a_rows2[src[i]];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) src[i] = (int)tt[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) arow[i] = p.A + (int64_t)src[i] * p.lda + acol;
   }
 
   // ---- MFMA ownership
@@ -215,10 +241,6 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
     acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // two register stages: the loads of step k + 2 are issued while step k computes, so each
-  // step has a step's worth of time more for its memory round trip
-  u32x4 areg[2][4];
-  BRegs breg[2];
   auto load_stage = [&](int k0, int b) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) areg[b][i] = *(const u32x4 *)(arow[i] + k0);
@@ -250,8 +272,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, co
     }
   };
 
-  load_stage(0, 0);
-  load_stage(min(BK, p.K - BK), 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) areg[0][i] = *(const u32x4 *)(arow[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) areg[1][i] = *(const u32x4 *)(arow[i] + k1);
   int k0 = 0;
   for (; k0 + 2 * BK <= p.K; k0 += 2 * BK) {
     step(k0, 0);
