@@ -415,7 +415,9 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
   if (has_shared)
     shared_gemm_args(L, x, T, (uint16_t *)at(o.shared_act), shared_out, sgu, sdn);
   begin(3);
-  e = launch_grouped_gemm2(gu, has_shared ? &sgu : nullptr, kEpiSwiglu, s);
+  // the shared expert's tiles (whole 128-row tiles) first: the dispatcher deals workgroups in
+  // order, so the lighter routed tiles fill the last, partial round of the grid
+  e = has_shared ? launch_grouped_gemm2(sgu, &gu, kEpiSwiglu, s) : launch_grouped_gemm2(gu, nullptr, kEpiSwiglu, s);
   end(3);
 
   GemmArgs dn{};
@@ -433,7 +435,8 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
   dn.C = eout;
   dn.ldc = H;
   begin(4);
-  if (e == hipSuccess) e = launch_grouped_gemm2(dn, has_shared ? &sdn : nullptr, kEpiPlain, s);
+  if (e == hipSuccess)
+    e = has_shared ? launch_grouped_gemm2(sdn, &dn, kEpiPlain, s) : launch_grouped_gemm2(dn, nullptr, kEpiPlain, s);
   end(4);
 
   if (has_shared) {
