@@ -88,7 +88,7 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
     uint32_t *__restrict__ offsets, uint32_t *__restrict__ tile_expert,
     uint32_t *__restrict__ tile_row0, uint32_t *__restrict__ tile_count) {
   __shared__ uint32_t base[kMaxBuckets];
-  __shared__ uint32_t wsum[2][kChunk / 64];
+  __shared__ uint32_t wsum[3][kChunk / 64];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int nb = E + 1;
   const int c = blockIdx.x;
@@ -116,36 +116,48 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
   uint32_t total, pre;
   sums(e, total, pre);
   const uint32_t tiles = e < E ? (total + kGemmBM - 1) / kGemmBM : 0u;
+  // tiles of more than kGemmBM / 2 rows (every full tile, and a last tile that large) come
+  // first in the table and the smaller last tiles after all of them: the GEMMs deal tiles in
+  // table order, so the light tiles fill the grid's last, partial round
+  const uint32_t big = e < E ? total / kGemmBM + (total % kGemmBM > kGemmBM / 2 ? 1u : 0u) : 0u;
   uint32_t extra_total = 0, extra_pre = 0;
   if (threadIdx.x == 0 && nb > kChunk) sums(kChunk, extra_total, extra_pre);
-  // block inclusive scans of total and tiles
-  uint32_t it = total, ip = tiles;
+  // block inclusive scans of total, tiles and big tiles
+  uint32_t it = total, ip = tiles, ib = big;
   for (int off = 1; off < 64; off <<= 1) {
     const uint32_t o = (uint32_t)__shfl_up((int)it, off, kWave);
     const uint32_t q = (uint32_t)__shfl_up((int)ip, off, kWave);
+    const uint32_t g = (uint32_t)__shfl_up((int)ib, off, kWave);
     if (lane >= off) {
       it += o;
       ip += q;
+      ib += g;
     }
   }
   if (lane == 63) {
     wsum[0][w] = it;
     wsum[1][w] = ip;
+    wsum[2][w] = ib;
   }
   __syncthreads();
-  uint32_t bt = 0, bp = 0;
+  uint32_t bt = 0, bp = 0, bb = 0, big_all = 0;
   for (int v = 0; v < w; ++v) {
     bt += wsum[0][v];
     bp += wsum[1][v];
+    bb += wsum[2][v];
   }
-  const uint32_t off_e = bt + it - total, tile0 = bp + ip - tiles;
+  for (int v = 0; v < kChunk / 64; ++v) big_all += wsum[2][v];
+  const uint32_t off_e = bt + it - total;
+  const uint32_t big0 = bb + ib - big;                      // big tiles of the buckets before e
+  const uint32_t small0 = big_all + (bp + ip - tiles) - big0;  // after every big tile
   if (e < nb) {
     base[e] = off_e + pre;
     if (c == 0) {
       offsets[e] = off_e;
       for (uint32_t i = 0; i < tiles; ++i) {
-        tile_expert[tile0 + i] = (uint32_t)e;
-        tile_row0[tile0 + i] = off_e + i * kGemmBM;
+        const uint32_t t = i < big ? big0 + i : small0;  // at most one small tile per bucket
+        tile_expert[t] = (uint32_t)e;
+        tile_row0[t] = off_e + i * kGemmBM;
       }
       if (e == nb - 1) {  // the last bucket's thread knows the totals
         offsets[nb] = (uint32_t)A;
