@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) 
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // STEP: n, [T][H]
   __shared__ float wsum[4];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-  const int e = blockIdx.x * 4 + wave;
+  const int e = blockIdx.x * (int)(blockDim.x >> 6) + wave;
   if (STEP) {
     const int nch = p.H / 8;
     const bool publish = blockIdx.x == 0;
@@ -726,7 +726,11 @@ void launch_down(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
 template <int MT, int NC>
 void launch_router_nc(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
   if (!a.norm_w) {
-    launch_timed(decode_router_kernel<MT, NC, false>, dim3(blocks), s, ev, a);
+    // one wave per workgroup: the E rows' loads come from E CUs rather than E / 4
+    if (ev)
+      hipExtLaunchKernelGGL(decode_router_kernel<MT, NC, false>, dim3(a.E), dim3(64), 0, s, ev[0], ev[1], 0, a);
+    else
+      hipLaunchKernelGGL((decode_router_kernel<MT, NC, false>), dim3(a.E), dim3(64), 0, s, a);
     return;
   }
   const size_t lds = (size_t)a.T * a.H * 2;
