@@ -356,12 +356,12 @@ struct StageClock {
 // The sparse graph after routing (forward_moe_with_streamed_weights, paged_execution.rs:207-281,
 // and the resident arm of resident_execution.rs:70-143): sort the assignments by id (expert or
 // page slot), gate/up with the SwiGLU epilogue over rows x[sorted_order[r] / kk], down, and the
-// weighted sum -- sorted rounding iff A >= 64 (routing.rs:13).  with_shared: the shared
-// expert's gate/up and down run in the routed launches and y = the shared combine; otherwise
-// y = the sparse output.
+// weighted sum -- sorted rounding iff A >= 64 (routing.rs:13) and not force_unsorted (an MTP
+// verification window).  with_shared: the shared expert's gate/up and down run in the routed
+// launches and y = the shared combine; otherwise y = the sparse output.
 hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk, const uint32_t *ids,
                       const uint16_t *scores, const Layout &o, char *ws, bool with_shared, uint16_t *y,
-                      hipStream_t s, StageClock *clock) {
+                      hipStream_t s, StageClock *clock, bool force_unsorted = false) {
   auto at = [&](size_t off) { return (void *)(ws + off); };
   auto begin = [&](int i) {
     if (clock) clock->begin(i);
@@ -446,7 +446,7 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
   }
   begin(6);
   if (e == hipSuccess)
-    e = launch_combine(eout, inverse, scores, T, kk, H, A >= 64, shared_out, z, sparse, y, s);
+    e = launch_combine(eout, inverse, scores, T, kk, H, A >= 64 && !force_unsorted, shared_out, z, sparse, y, s);
   end(6);
   return e;
 }
@@ -638,7 +638,9 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   }
   end(1);
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
-  e = run_sparse(L, x, T, k, ids, scores, o, ws, true, y, s, clock);
+  // a verification window keeps the unsorted reduction at every length
+  // (forward_moe_resident_target_verification, resident_execution.rs:146-208)
+  e = run_sparse(L, x, T, k, ids, scores, o, ws, true, y, s, clock, verification);
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
   return finish();
 }
@@ -682,6 +684,10 @@ int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
   view->shared_gate_logits = o.z;
   view->expert_slots = o.slots;
   view->missing_slots = o.missing;
+  view->tile_expert = o.decode ? 0 : o.tile_expert;
+  view->tile_row0 = o.decode ? 0 : o.tile_row0;
+  view->tile_count = o.decode ? 0 : o.tile_count;
+  view->max_tiles = o.decode ? 0 : (size_t)o.max_tiles;
   return ok();
 }
 
@@ -1142,6 +1148,17 @@ int astro_moe_decoder_ffn_forward(const astro_moe_layer *layer, const uint16_t *
   if (!hidden || !norm_weight || !out) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "hidden states, weight and output must be non-null");
   if (!(eps >= 0.0f)) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "epsilon must be a non-negative number");
   if (H > 8192) return fail(ASTRO_MOE_UNSUPPORTED, op, "the normalization kernel supports hidden sizes up to 8192");
+  // The router kernel of the fused decode step writes r while other workgroups still read the
+  // hidden states and the attention output to form r themselves, so r may not share memory
+  // with either input (an in-place residual update would feed r + a back into them).
+  const size_t rows_bytes = (size_t)tokens * H * 2;
+  auto overlaps = [&](const void *a, const void *b) {
+    const char *pa = (const char *)a, *pb = (const char *)b;
+    return a && b && pa < pb + rows_bytes && pb < pa + rows_bytes;
+  };
+  if (overlaps(residual_out, hidden) || overlaps(residual_out, attention_out))
+    return fail(ASTRO_MOE_INVALID_ARGUMENT, op,
+                "residual output must not overlap the hidden states or the attention output");
   char *ws = (char *)workspace;
   uint16_t *r = (uint16_t *)(ws + align_up(blk));
   uint16_t *n = (uint16_t *)((char *)r + align_up((size_t)tokens * H * 2));

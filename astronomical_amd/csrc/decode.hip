@@ -12,741 +12,9 @@
 // turned into bf16 pairs (128 + q) with one and/or per pair and multiplied by
 // v_dot2_f32_bf16; the per-group affine terms are applied per 32-input chunk:
 //   sum_j x_j (s q_j + b) = s * sum_j (128 + q_j) x_j + (b - 128 s) * sum_j x_j.
-#include "common.h"
-#include "kernels.h"
-#include "route_dev.h"
-
-#include <hip/hip_ext.h>
-
-#include <algorithm>
-#include <type_traits>
+#include "decode_dev.h"
 
 namespace astro {
-
-namespace {
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// (gate row, up row) pairs per wave in the gate/up GEMVs: one keeps each wave's serial
-// instruction chain short; the chip has wave slots to spare at decode sizes
-constexpr int kRowsPerWave = kDecodeRowsPerWave;
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
-                                         c, false);
-}
-
-__device__ __forceinline__ uint32_t pack_bf2_hw(float lo, float hi) {
-  bf16x2 v;
-  v[0] = (__bf16)lo;
-  v[1] = (__bf16)hi;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// 32 consecutive activations of one token, ready for the code dot products.  For 4-bit
-// codes the bf16 pairs are (x0,x4),(x1,x5),(x2,x6),(x3,x7) per 8 inputs, matching the
-// nibble pairs produced by (word >> 4m) & 0x000f000f; 8-bit codes use natural pairs.
-struct XChunk {
-  uint32_t p[16];
-  float sum;
-};
-
-struct XRaw {
-  u32x4 v[4];
-};
-
-__device__ __forceinline__ void load_xraw(XRaw &xr, const uint16_t *src) {
-  const u32x4 *q = (const u32x4 *)src;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) xr.v[i] = q[i];
-}
-
-template <int BITS>
-__device__ __forceinline__ void convert_xchunk(XChunk &xc, const XRaw &xr) {
-  uint32_t r[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    r[4 * i] = xr.v[i][0];
-    r[4 * i + 1] = xr.v[i][1];
-    r[4 * i + 2] = xr.v[i][2];
-    r[4 * i + 3] = xr.v[i][3];
-  }
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) s = dot2(r[j], 0x3f803f80u, s);
-  xc.sum = s;
-  if (BITS == 4) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t a = r[4 * i], b = r[4 * i + 1], c = r[4 * i + 2], d = r[4 * i + 3];
-      xc.p[4 * i + 0] = (a & 0xffffu) | (c << 16);
-      xc.p[4 * i + 1] = (a >> 16) | (c & 0xffff0000u);
-      xc.p[4 * i + 2] = (b & 0xffffu) | (d << 16);
-      xc.p[4 * i + 3] = (b >> 16) | (d & 0xffff0000u);
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) xc.p[j] = r[j];
-  }
-}
-
-template <int BITS>
-__device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *src) {
-  XRaw xr;
-  load_xraw(xr, src);
-  convert_xchunk<BITS>(xc, xr);
-}
-
-// codes of one 32-input chunk of one weight row: 4 words (4-bit) or 8 words (8-bit)
-struct WChunk {
-  u32x4 q[2];
-  float s, b;
-};
-
-template <int BITS>
-__device__ __forceinline__ void load_wchunk(WChunk &w, const uint32_t *row, const uint16_t *srow,
-                                            const uint16_t *brow, int chunk, int group) {
-  const u32x4 *p = (const u32x4 *)(row + chunk * BITS);
-  w.q[0] = p[0];
-  if (BITS == 8) w.q[1] = p[1];
-  const int g = (chunk * 32) / group;
-  w.s = bf2f(srow[g]);
-  w.b = bf2f(brow[g]);
-}
-
-// sum over the chunk of x * (s*q + b)
-template <int BITS>
-__device__ __forceinline__ float chunk_dot(const WChunk &w, const XChunk &x) {
-  float acc = 0.0f;
-  if (BITS == 4) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t word = w.q[0][i];
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        acc = dot2(((word >> (4 * m)) & 0x000f000fu) | 0x43004300u, x.p[4 * i + m], acc);
-    }
-    return __builtin_fmaf(w.s, acc, __builtin_fmaf(-128.0f, w.s, w.b) * x.sum);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t word = w.q[i >> 2][i & 3];
-      const uint32_t lo = pack_bf2_hw((float)(word & 255u), (float)((word >> 8) & 255u));
-      const uint32_t hi = pack_bf2_hw((float)((word >> 16) & 255u), (float)(word >> 24));
-      acc = dot2(lo, x.p[2 * i], acc);
-      acc = dot2(hi, x.p[2 * i + 1], acc);
-    }
-    return __builtin_fmaf(w.s, acc, w.b * x.sum);
-  }
-}
-
-// One wave: RP consecutive rows of a gate projection and the matching rows of an up
-// projection (SwiGLU) — or of one plain projection — against MT activation rows.  Lane l
-// covers input chunks l, l+64, ... (NC chunks).  The body has no data-dependent branches:
-// rows past `nrows` reuse the last row, `xrows` arrives clamped to valid rows, lanes past
-// the chunk count load chunk 0 and contribute zero, so every load is issued up front.
-template <int BITS, int MT, int RP, bool SWIGLU, int NC>
-__device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb,
-                                          const uint32_t *uw, const uint16_t *us, const uint16_t *ub,
-                                          int64_t w_rs, int64_t sb_rs, int nrows, int nchunks,
-                                          int group, const uint16_t *x, int64_t ldx,
-                                          const int *xrows, int m, uint16_t *out, int64_t ldo,
-                                          const int *orows) {
-  const int lane = (int)(threadIdx.x & 63);
-  float accg[RP][MT], accu[RP][MT];
-#pragma unroll
-  for (int r = 0; r < RP; ++r)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) accg[r][t] = accu[r][t] = 0.0f;
-  int xr[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) xr[t] = xrows[t];
-#pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    const int craw = lane + 64 * cc;
-    const bool cv = craw < nchunks;
-    const int c = cv ? craw : 0;
-    WChunk wg[RP], wu[RP];
-#pragma unroll
-    for (int r = 0; r < RP; ++r) {
-      const int rr = r < nrows ? r : nrows - 1;
-      load_wchunk<BITS>(wg[r], gw + rr * w_rs, gs + rr * sb_rs, gb + rr * sb_rs, c, group);
-      if (SWIGLU) load_wchunk<BITS>(wu[r], uw + rr * w_rs, us + rr * sb_rs, ub + rr * sb_rs, c, group);
-    }
-    XChunk xc[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) load_xchunk<BITS>(xc[t], x + (int64_t)xr[t] * ldx + c * 32);
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-#pragma unroll
-      for (int r = 0; r < RP; ++r) {
-        const float dg = chunk_dot<BITS>(wg[r], xc[t]);
-        accg[r][t] += cv ? dg : 0.0f;
-        if (SWIGLU) {
-          const float du = chunk_dot<BITS>(wu[r], xc[t]);
-          accu[r][t] += cv ? du : 0.0f;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < RP; ++r) {
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const float g = wave_sum_fast(accg[r][t]);
-      uint32_t o;
-      if (SWIGLU) {
-        const float u = wave_sum_fast(accu[r][t]);
-        o = swiglu_bf(round_bf(g), round_bf(u));
-      } else {
-        o = f2bf(g);
-      }
-      if (lane == 0 && r < nrows && t < m) out[(int64_t)orows[t] * ldo + r] = (uint16_t)o;
-    }
-  }
-}
-
-// rows_task over at most 4 tokens at a time: more tokens run as passes of 4 over the same
-// rows (the second reads the codes from L2), which keeps the kernel's registers at the
-// 4-token footprint; each token's sums are the same either way.
-template <int BITS, int MT, int RP, bool SWIGLU, int NC>
-__device__ __forceinline__ void rows_task_q(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb,
-                                            const uint32_t *uw, const uint16_t *us, const uint16_t *ub,
-                                            int64_t w_rs, int64_t sb_rs, int nrows, int nchunks, int group,
-                                            const uint16_t *x, int64_t ldx, const int *xrows, int m, uint16_t *out,
-                                            int64_t ldo, const int *orows) {
-  if constexpr (MT <= 4) {
-    rows_task<BITS, MT, RP, SWIGLU, NC>(gw, gs, gb, uw, us, ub, w_rs, sb_rs, nrows, nchunks, group, x, ldx, xrows,
-                                        m, out, ldo, orows);
-  } else {
-    for (int t0 = 0; t0 < MT; t0 += 4) {
-      if (t0 >= m) break;
-      rows_task<BITS, 4, RP, SWIGLU, NC>(gw, gs, gb, uw, us, ub, w_rs, sb_rs, nrows, nchunks, group, x, ldx,
-                                         xrows + t0, m - t0 < 4 ? m - t0 : 4, out, ldo, orows + t0);
-    }
-  }
-}
-
-// ---------------------------------------------------------------- D1: router
-
-// Router GEMV: one wave per expert row (bf16 weights), every token.  STEP (the decoder step):
-// every workgroup first forms r = bf16(h + a) and the RMS-normalised rows n of the T tokens in
-// LDS (the order of add_rms_norm_kernel: rms_* in common.h) and reads its activations from
-// there; workgroup 0 also writes r and n for the later kernels.
-template <int MT, int NC, bool STEP>
-__global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // STEP: n, [T][H]
-  __shared__ float wsum[4];
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-  const int e = blockIdx.x * (int)(blockDim.x >> 6) + wave;
-  if (STEP) {
-    const int nch = p.H / 8;
-    const bool publish = blockIdx.x == 0;
-    float part[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      part[t] = 0.0f;
-      if (t >= p.T) continue;
-      for (int c = threadIdx.x; c < nch; c += 256) {
-        const int64_t o = (int64_t)t * p.H + 8 * c;
-        const u32x4 r = rms_residual(*(const u32x4 *)(p.h_in + o), p.a_in ? (const u32x4 *)(p.a_in + o) : nullptr);
-        *(u32x4 *)(xs + o) = r;
-        if (publish) *(u32x4 *)(p.r_out + o) = r;
-        part[t] = rms_partial(r, part[t]);
-      }
-    }
-    float inv[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) inv[t] = t < p.T ? rms_inverse(rms_total(part[t], wsum), p.H, p.eps) : 0.0f;
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      if (t >= p.T) continue;
-      for (int c = threadIdx.x; c < nch; c += 256) {
-        const int64_t o = (int64_t)t * p.H + 8 * c;
-        const u32x4 n = rms_apply(*(const u32x4 *)(xs + o), *(const u32x4 *)(p.norm_w + 8 * c), inv[t]);
-        *(u32x4 *)(xs + o) = n;
-        if (publish) *(u32x4 *)(p.x_out + o) = n;
-      }
-    }
-    __syncthreads();
-  }
-  if (e >= p.E) return;
-  const int nchunks = p.H / 32;
-  const uint16_t *w = p.router_w + (int64_t)e * p.H;
-  float acc[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-#pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    const int craw = lane + 64 * cc;
-    const bool cv = craw < nchunks;
-    const int c = cv ? craw : 0;
-    const u32x4 *wp = (const u32x4 *)(w + c * 32);
-    u32x4 wv[4], xv[MT][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wv[i] = wp[i];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int tr = t < p.T ? t : p.T - 1;
-      const u32x4 *xp = (const u32x4 *)((STEP ? xs : p.x) + (int64_t)tr * p.H + c * 32);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xv[t][i] = xp[i];
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      float a = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a = dot2(wv[i][j], xv[t][i][j], a);
-      acc[t] += cv ? a : 0.0f;
-    }
-  }
-  const float bias = p.router_bias ? bf2f(p.router_bias[e]) : 0.0f;
-#pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const float v = wave_sum_fast(acc[t]);
-    if (lane == 0 && t < p.T) {
-      uint32_t o = f2bf(v);
-      if (p.router_bias) o = f2bf(bf2f(o) + bias);
-      p.logits[(int64_t)t * p.E + e] = (uint16_t)o;
-    }
-  }
-}
-
-// ---------------------------------------------------------------- D2: route + gate/up
-
-// Routing of the <= 8 tokens from their logits (route_token), the stable sort of the <= 64
-// assignments and the table of distinct experts, into LDS; with publish, also written to the
-// workspace for the later kernels (ids, scores, sort, inverse, offsets, the table).
-template <int MT, int PER>
-__device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, uint32_t *idx_sh, uint32_t *so_sh,
-                                             uint32_t *sid_sh, uint32_t *key_sh, uint32_t (*route_sh)[kDecodeMaxK],
-                                             uint16_t *sc_sh, uint32_t *g_expert_sh, uint32_t *g_start_sh,
-                                             uint32_t *g_count_sh, uint32_t &ng_sh) {
-  constexpr int KM = kDecodeMaxK, AMAX = MT * KM;
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-  const int A = p.A;
-  const int nwaves = (int)(blockDim.x >> 6);
-  for (int t = wave; t < p.T; t += nwaves) {
-    uint32_t my_idx, my_score;
-    route_token<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, route_sh[wave],
-                         my_idx, my_score);
-    if (lane < p.k) {
-      idx_sh[t * p.k + lane] = my_idx;
-      sc_sh[t * p.k + lane] = (uint16_t)my_score;
-    }
-  }
-  __syncthreads();
-  if (wave == 0) {
-    // stable sort by (expert, slot): rank = number of smaller keys
-    const uint32_t key = lane < A ? (idx_sh[lane] << 6) | (uint32_t)lane : 0xffffffffu;
-    key_sh[lane] = key;
-    __builtin_amdgcn_wave_barrier();
-    // the AMAX >= A keys in broadcast reads, issued before any comparison
-    u32x4 kv[AMAX / 4];
-#pragma unroll
-    for (int b2 = 0; b2 < AMAX / 4; ++b2) kv[b2] = ((const u32x4 *)key_sh)[b2];
-    uint32_t rank = 0;
-#pragma unroll
-    for (int b2 = 0; b2 < AMAX / 4; ++b2)
-      rank += (kv[b2][0] < key) + (kv[b2][1] < key) + (kv[b2][2] < key) + (kv[b2][3] < key);
-    if (lane < A) {
-      so_sh[rank] = (uint32_t)lane;
-      sid_sh[rank] = key >> 6;
-    }
-    __builtin_amdgcn_wave_barrier();
-    // distinct experts in ascending order: (expert, first sorted row, count)
-    const uint32_t sid = lane < A ? sid_sh[lane] : 0xffffffffu;
-    const bool start = lane < A && (lane == 0 || sid != sid_sh[lane - 1]);
-    const uint64_t mask = __ballot(start);
-    const int gi = __popcll(mask & ((1ull << lane) - 1ull));
-    const uint64_t above = lane == 63 ? 0ull : (mask >> (lane + 1));
-    const int next = above ? lane + 1 + __ffsll((long long)above) - 1 : A;
-    if (start) {
-      g_expert_sh[gi] = sid;
-      g_start_sh[gi] = (uint32_t)lane;
-      g_count_sh[gi] = (uint32_t)(next - lane);
-    }
-    if (lane == 0) ng_sh = (uint32_t)__popcll(mask);
-    if (publish) {
-      if (lane < A) {
-        p.idx[lane] = idx_sh[lane];
-        p.scores[lane] = sc_sh[lane];
-        p.sorted_order[rank] = (uint32_t)lane;
-        p.inverse_order[lane] = rank;
-        p.sorted_ids[rank] = key >> 6;
-      }
-      if (start) {
-        p.g_expert[gi] = sid;
-        p.g_start[gi] = (uint32_t)lane;
-        p.g_count[gi] = (uint32_t)(next - lane);
-      }
-      if (lane == 0) *p.n_groups = (uint32_t)__popcll(mask);
-    }
-  }
-  __syncthreads();
-  if (publish) {
-    // expert offsets [E+2] (E+1: trailing out-of-range bucket, empty here)
-    for (int e = threadIdx.x; e <= p.E + 1; e += (int)blockDim.x) {
-      uint32_t c = 0;
-#pragma unroll
-      for (int i = 0; i < AMAX; ++i) c += (i < A) & (sid_sh[i] < (uint32_t)e);
-      p.offsets[e] = e <= p.E ? c : (uint32_t)A;
-    }
-  }
-}
-
-// Routing once for a batch of tokens (T >= kDecodeRouteOnceT): one workgroup runs decode_route
-// and publishes it; the gate/up kernel's routed workgroups then read the table instead of
-// each recomputing every token's routing.
-template <int MT, int PER>
-__global__ __launch_bounds__(64 * MT) void decode_route_kernel(const DecodeArgs p) {
-  constexpr int KM = kDecodeMaxK;
-  __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
-  __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
-  __shared__ __attribute__((aligned(16))) uint32_t route_sh[MT][KM];
-  __shared__ uint16_t sc_sh[64];
-  __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
-  decode_route<MT, PER>(p, true, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh,
-                        g_count_sh, ng_sh);
-}
-
-// Workgroups (x, 0): the shared expert, which needs no routing — x < shared_pair_blocks
-// computes 4 (gate row, up row) pairs with the SwiGLU epilogue, x == shared_pair_blocks
-// the output gate z.  Workgroups (x, g + 1): rows of the gate/up GEMV of the g-th distinct
-// expert for every token routed to it (SwiGLU epilogue).  Without PRE (one token) every one
-// of them first recomputes the routing from the logits (route_token), the stable sort of the
-// assignments and the table of distinct experts — a few microseconds of one wave's work that
-// saves a dependent kernel boundary — and workgroup (0, 1) publishes them.  With PRE (batches
-// from kDecodeRouteOnceT tokens) decode_route_kernel has published the routing and the
-// workgroups read it instead.  RPW: (gate, up) row pairs per routed wave (more for larger
-// batches: fewer, fuller workgroups).
-template <int BITS, int MT, int NC, int PER, bool PRE, int RPW>
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
-  constexpr int KM = kDecodeMaxK;
-  __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
-  __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
-  __shared__ __attribute__((aligned(16))) uint32_t route_sh[4][KM];
-  __shared__ uint16_t sc_sh[64];
-  __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
-  __shared__ int rows_sh[MT], orows_sh[MT];
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int nchunks = p.H / 32;
-  if (blockIdx.y == 0) {
-    if (threadIdx.x < MT) {
-      const int t = threadIdx.x < p.T ? threadIdx.x : p.T - 1;
-      rows_sh[threadIdx.x] = t;
-      orows_sh[threadIdx.x] = p.A + t;
-    }
-    __syncthreads();
-    const int sb = blockIdx.x;
-    if (sb < p.shared_pair_blocks) {
-      const int r0 = (sb * 4 + wave) * kRowsPerWave;
-      if (r0 >= p.Is) return;
-      const int nrows = min(kRowsPerWave, p.Is - r0);
-      if (p.sg_bits == 4)
-        rows_task_q<4, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
-                                                 p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
-                                                 p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
-                                                 p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
-                                                 p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
-                                                 orows_sh);
-      else
-        rows_task_q<8, MT, kRowsPerWave, true, NC>(p.sg_w + r0 * p.sg_w_rs, p.sg_s + r0 * p.sg_sb_rs,
-                                                 p.sg_b + r0 * p.sg_sb_rs, p.su_w + r0 * p.sg_w_rs,
-                                                 p.su_s + r0 * p.sg_sb_rs, p.su_b + r0 * p.sg_sb_rs,
-                                                 p.sg_w_rs, p.sg_sb_rs, nrows, nchunks, p.sg_group,
-                                                 p.x, p.H, rows_sh, p.T, p.act + r0, p.act_ld,
-                                                 orows_sh);
-      return;
-    }
-    if (sb != p.shared_pair_blocks || wave != 0 || !p.sz_w) return;
-    if (p.sz_bits == 4)
-      rows_task_q<4, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
-                                     nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
-    else
-      rows_task_q<8, MT, 1, false, NC>(p.sz_w, p.sz_s, p.sz_b, nullptr, nullptr, nullptr, 0, 0, 1,
-                                     nchunks, p.sz_group, p.x, p.H, rows_sh, p.T, p.z, 1, rows_sh);
-    return;
-  }
-  if ((int)blockIdx.x * 4 * RPW >= p.I) return;
-  uint32_t e, start, m;
-  if (PRE) {
-    const int g = blockIdx.y - 1;
-    if (g >= (int)*p.n_groups) return;
-    e = p.g_expert[g];
-    start = p.g_start[g];
-    m = p.g_count[g];
-    if (m > (uint32_t)MT) return;  // a token selects an expert at most once: m <= T <= MT
-    if (threadIdx.x < MT) {
-      const uint32_t i = threadIdx.x < m ? threadIdx.x : m - 1;
-      rows_sh[threadIdx.x] = (int)(p.sorted_order[start + i] / (uint32_t)p.k);
-      orows_sh[threadIdx.x] = (int)(start + i);
-    }
-  } else {
-    decode_route<MT, PER>(p, blockIdx.x == 0 && blockIdx.y == 1, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh,
-                          g_expert_sh, g_start_sh, g_count_sh, ng_sh);
-    const int g = blockIdx.y - 1;
-    if (g >= (int)ng_sh) return;
-    e = g_expert_sh[g];
-    start = g_start_sh[g];
-    m = g_count_sh[g];
-    if (m > (uint32_t)MT) return;  // a token selects an expert at most once: m <= T <= MT
-    if (threadIdx.x < MT) {
-      const uint32_t i = threadIdx.x < m ? threadIdx.x : m - 1;
-      rows_sh[threadIdx.x] = (int)(so_sh[start + i] / (uint32_t)p.k);
-      orows_sh[threadIdx.x] = (int)(start + i);
-    }
-  }
-  __syncthreads();
-  const int r0 = (blockIdx.x * 4 + wave) * RPW;
-  if (r0 >= p.I) return;
-  const int nrows = min(RPW, p.I - r0);
-  const int64_t wo = (int64_t)e * p.gu_w_es + (int64_t)r0 * p.gu_w_rs;
-  const int64_t so = (int64_t)e * p.gu_sb_es + (int64_t)r0 * p.gu_sb_rs;
-  // the expert's m <= MT tokens: the smallest token count instantiated that covers them (each
-  // token's sums do not depend on it)
-  auto routed_rows = [&](auto mt_tag) {
-    constexpr int M2 = decltype(mt_tag)::value;
-    rows_task_q<BITS, M2, RPW, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
-                                                p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows, nchunks,
-                                                p.gu_group, p.x, p.H, rows_sh, (int)m, p.act + r0, p.act_ld,
-                                                orows_sh);
-  };
-  if (m <= 1) routed_rows(std::integral_constant<int, 1>());
-  else if (MT > 2 && m <= 2) routed_rows(std::integral_constant<int, (MT > 2 ? 2 : MT)>());
-  else if (MT > 4 && m <= 4) routed_rows(std::integral_constant<int, (MT > 4 ? 4 : MT)>());
-  else routed_rows(std::integral_constant<int, MT>());
-}
-
-// ---------------------------------------------------------------- D3: down + combine
-
-// One workgroup of 4 waves per (4 output rows, token).  The token's k experts and the
-// shared expert are P = kDecodeMaxK + 1 participant rows per output row; wave w computes
-// participants w, w+4, w+8.  Quarter q of a wave (one DPP row of 16 lanes) takes output
-// row 4x + q and its 16 lanes split the input chunks (lane l16 takes chunks l16, l16+16,
-// ...).  The rounded participant values meet in LDS, where wave 0 forms the weighted
-// combine (slot order) and the shared expert's gated add.  Branch-free: participants past
-// k, or a missing shared expert, reuse slot 0's rows and are masked out.
-template <int BITS, int NC, bool SORTED>
-__global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
-  constexpr int KM = kDecodeMaxK, P = KM + 1, PW = (P + 3) / 4;
-  __shared__ float vals[4][4 * PW];
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
-  const int t = blockIdx.y, h = blockIdx.x * 4 + q;
-  const bool has_shared = p.Is > 0;
-  // loads the combine needs, issued first (a missing shared expert reads a score instead)
-  const uint16_t zbits = has_shared ? p.z[t] : p.scores[0];
-  const uint16_t rbits = p.ffn_out ? p.r_out[(int64_t)t * p.H + h] : 0;  // the decoder step's residual
-  float sc[KM];
-#pragma unroll
-  for (int j = 0; j < KM; ++j) sc[j] = bf2f(p.scores[t * p.k + (j < p.k ? j : p.k - 1)]);
-
-  // participant rows, selected without branches
-  const uint32_t *sd_w = has_shared ? p.sd_w : p.down_w;
-  const uint16_t *sd_s = has_shared ? p.sd_s : p.down_s;
-  const uint16_t *sd_b = has_shared ? p.sd_b : p.down_b;
-  const int64_t sd_w_rs = has_shared ? p.sd_w_rs : p.dn_w_rs;
-  const int64_t sd_sb_rs = has_shared ? p.sd_sb_rs : p.dn_sb_rs;
-  const int sd_nch = has_shared ? p.Is / 32 : p.I / 32;
-  const int sd_group = has_shared ? p.sd_group : p.dn_group;
-  uint32_t e[PW], r[PW];
-#pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const int j = wave + 4 * i;
-    const int a = t * p.k + (j < p.k ? j : 0);
-    e[i] = p.idx[a];
-    r[i] = p.inverse_order[a];
-  }
-  const uint32_t *wrow[PW];
-  const uint16_t *srow[PW], *brow[PW];
-  const uint16_t *xrow[PW];
-  int nch[PW], grp[PW];
-  uint32_t orow[PW];
-  bool live[PW];
-#pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const int j = wave + 4 * i;
-    const bool shared = j == KM && has_shared;
-    live[i] = (j < KM && j < p.k) || shared;
-    orow[i] = shared ? (uint32_t)(p.A + t) : r[i];
-    const uint32_t *wb = shared ? sd_w : p.down_w + (int64_t)e[i] * p.dn_w_es;
-    const uint16_t *sb = shared ? sd_s : p.down_s + (int64_t)e[i] * p.dn_sb_es;
-    const uint16_t *bb = shared ? sd_b : p.down_b + (int64_t)e[i] * p.dn_sb_es;
-    const int64_t wrs = shared ? sd_w_rs : p.dn_w_rs;
-    const int64_t sbrs = shared ? sd_sb_rs : p.dn_sb_rs;
-    wrow[i] = wb + (int64_t)h * wrs;
-    srow[i] = sb + (int64_t)h * sbrs;
-    brow[i] = bb + (int64_t)h * sbrs;
-    xrow[i] = p.act + (int64_t)orow[i] * p.act_ld;
-    nch[i] = shared ? sd_nch : p.I / 32;
-    grp[i] = shared ? sd_group : p.dn_group;
-  }
-  float acc[PW];
-#pragma unroll
-  for (int i = 0; i < PW; ++i) acc[i] = 0.0f;
-#pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    const int craw = l16 + 16 * cc;
-    // every load of the chunk step first, then the arithmetic
-    WChunk wch[PW];
-    XRaw xr[PW];
-#pragma unroll
-    for (int i = 0; i < PW; ++i) {
-      const int c = craw < nch[i] ? craw : 0;
-      load_wchunk<BITS>(wch[i], wrow[i], srow[i], brow[i], c, grp[i]);
-      load_xraw(xr[i], xrow[i] + c * 32);
-    }
-    // keep the scheduler from interleaving the first participant's arithmetic (and its
-    // waits) with the later participants' loads
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < PW; ++i) {
-      XChunk xc;
-      convert_xchunk<BITS>(xc, xr[i]);
-      const float d = chunk_dot<BITS>(wch[i], xc);
-      acc[i] += craw < nch[i] ? d : 0.0f;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const float v = round_bf(row_sum(acc[i]));
-    if (l16 == 0) {
-      vals[q][wave + 4 * i] = v;
-      if (live[i]) p.down_out[(int64_t)orow[i] * p.H + h] = (uint16_t)f2bf(v);
-    }
-  }
-  __syncthreads();
-  if (wave != 0 || l16 != 0) return;
-  float v[KM];
-#pragma unroll
-  for (int j = 0; j < KM; ++j) v[j] = vals[q][j];
-  const uint32_t sparse = combine_element<SORTED, KM>(v, sc, p.k);
-  uint32_t out = sparse;
-  if (has_shared) out = shared_gated_add(sparse, vals[q][KM], round_bf(det_sigmoid(bf2f(zbits))));
-  p.sparse[(int64_t)t * p.H + h] = (uint16_t)sparse;
-  p.y[(int64_t)t * p.H + h] = (uint16_t)out;
-  if (p.ffn_out) p.ffn_out[(int64_t)t * p.H + h] = (uint16_t)f2bf(bf2f(rbits) + bf2f(out));
-}
-
-// 256-thread launch; ev (nullable) = {start, stop} events recorded around the kernel itself
-template <typename Kernel>
-void launch_timed(Kernel kernel, dim3 grid, hipStream_t s, const hipEvent_t *ev, const DecodeArgs &a) {
-  if (ev)
-    hipExtLaunchKernelGGL(kernel, grid, dim3(256), 0, s, ev[0], ev[1], 0, a);
-  else
-    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, a);
-}
-
-template <int BITS, int MT, int NC, int PER, int RPW>
-void launch_gate_up_rpw(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  // x: routed row blocks, or the shared expert's pair blocks and its output-gate block
-  const int routed_x = (a.I + 4 * RPW - 1) / (4 * RPW);
-  const int shared_x = a.Is > 0 ? a.shared_pair_blocks + 1 : 0;
-  const dim3 grid(std::max(routed_x, shared_x), a.max_groups + 1);
-  if (a.T >= kDecodeRouteOnceT)
-    launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, true, RPW>, grid, s, ev, a);
-  else
-    launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, false, RPW>, grid, s, ev, a);
-}
-
-template <int BITS, int MT, int NC, int PER>
-void launch_gate_up_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  // one row pair per routed wave for a single token (the chip has wave slots to spare); a
-  // batch selects up to 8x more distinct experts, so each wave takes more rows
-  if (MT <= 1) launch_gate_up_rpw<BITS, MT, NC, PER, kRowsPerWave>(a, s, ev);
-  else if (MT <= 2) launch_gate_up_rpw<BITS, MT, NC, PER, 2>(a, s, ev);
-  else launch_gate_up_rpw<BITS, MT, NC, PER, 4>(a, s, ev);
-}
-
-// one workgroup, one wave per token slot and at least 4 (the E + 2 expert offsets are spread
-// over every thread of the block)
-template <int MT, int PER>
-void launch_route_per(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  constexpr int W = MT > 4 ? MT : 4;
-  if (ev)
-    hipExtLaunchKernelGGL((decode_route_kernel<W, PER>), dim3(1), dim3(64 * W), 0, s, ev[0], ev[1], 0, a);
-  else
-    hipLaunchKernelGGL((decode_route_kernel<W, PER>), dim3(1), dim3(64 * W), 0, s, a);
-}
-
-template <int MT>
-void launch_route_mt(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  const int per = (a.E + 63) / 64;
-  if (per <= 1) launch_route_per<MT, 1>(a, s, ev);
-  else if (per <= 2) launch_route_per<MT, 2>(a, s, ev);
-  else if (per <= 4) launch_route_per<MT, 4>(a, s, ev);
-  else if (per <= 8) launch_route_per<MT, 8>(a, s, ev);
-  else launch_route_per<MT, 16>(a, s, ev);
-}
-
-template <int BITS, int MT, int NC>
-void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  const int per = (a.E + 63) / 64;
-  if (per <= 1) launch_gate_up_per<BITS, MT, NC, 1>(a, s, ev);
-  else if (per <= 2) launch_gate_up_per<BITS, MT, NC, 2>(a, s, ev);
-  else if (per <= 4) launch_gate_up_per<BITS, MT, NC, 4>(a, s, ev);
-  else if (per <= 8) launch_gate_up_per<BITS, MT, NC, 8>(a, s, ev);
-  else launch_gate_up_per<BITS, MT, NC, 16>(a, s, ev);
-}
-
-template <int BITS, int NC>
-void launch_down_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  const dim3 grid(a.H / 4, a.T);
-  // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64; a verification
-  // window keeps the unsorted one (resident_execution.rs:161-162)
-  if (a.A >= 64 && !a.unsorted)
-    launch_timed(decode_down_kernel<BITS, NC, true>, grid, s, ev, a);
-  else
-    launch_timed(decode_down_kernel<BITS, NC, false>, grid, s, ev, a);
-}
-
-template <int BITS, int MT>
-void launch_gate_up_mt(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  if (a.H <= 2048) launch_gate_up_nc<BITS, MT, 1>(a, s, ev);
-  else launch_gate_up_nc<BITS, MT, 2>(a, s, ev);
-}
-
-template <int BITS>
-void launch_gate_up(const DecodeArgs &a, int mt, hipStream_t s, const hipEvent_t *ev) {
-  if (mt == 1) launch_gate_up_mt<BITS, 1>(a, s, ev);
-  else if (mt == 2) launch_gate_up_mt<BITS, 2>(a, s, ev);
-  else if (mt == 4) launch_gate_up_mt<BITS, 4>(a, s, ev);
-  else launch_gate_up_mt<BITS, 8>(a, s, ev);
-}
-
-template <int BITS>
-void launch_down(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  if (std::max(a.I, a.Is) <= 512) launch_down_nc<BITS, 1>(a, s, ev);
-  else launch_down_nc<BITS, 2>(a, s, ev);
-}
-
-template <int MT, int NC>
-void launch_router_nc(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
-  if (!a.norm_w) {
-    // one wave per workgroup: the E rows' loads come from E CUs rather than E / 4
-    if (ev)
-      hipExtLaunchKernelGGL(decode_router_kernel<MT, NC, false>, dim3(a.E), dim3(64), 0, s, ev[0], ev[1], 0, a);
-    else
-      hipLaunchKernelGGL((decode_router_kernel<MT, NC, false>), dim3(a.E), dim3(64), 0, s, a);
-    return;
-  }
-  const size_t lds = (size_t)a.T * a.H * 2;
-  if (ev)
-    hipExtLaunchKernelGGL(decode_router_kernel<MT, NC, true>, dim3(blocks), dim3(256), lds, s, ev[0], ev[1], 0, a);
-  else
-    hipLaunchKernelGGL((decode_router_kernel<MT, NC, true>), dim3(blocks), dim3(256), lds, s, a);
-}
-
-template <int MT>
-void launch_router(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
-  if (a.H <= 2048) launch_router_nc<MT, 1>(a, blocks, s, ev);
-  else launch_router_nc<MT, 2>(a, blocks, s, ev);
-}
-
-}  // namespace
 
 bool decode_supported(const DecodeArgs &a) {
   return a.T >= 1 && a.T <= 8 && a.A <= 64 && a.router_w != nullptr && a.H % 32 == 0 &&
@@ -781,8 +49,17 @@ hipError_t launch_decode_block(const DecodeArgs &a, hipStream_t s, const hipEven
     if (e != hipSuccess) return e;
   }
   // D2: shared gate/up, routing (T = 1), routed gate/up
-  if (a.gu_bits == 8) launch_gate_up<8>(a, mt, s, e2);
-  else launch_gate_up<4>(a, mt, s, e2);
+  if (a.gu_bits == 8) {
+    if (mt == 1) launch_decode_gate_up<8, 1>(a, s, e2);
+    else if (mt == 2) launch_decode_gate_up<8, 2>(a, s, e2);
+    else if (mt == 4) launch_decode_gate_up<8, 4>(a, s, e2);
+    else launch_decode_gate_up<8, 8>(a, s, e2);
+  } else {
+    if (mt == 1) launch_decode_gate_up<4, 1>(a, s, e2);
+    else if (mt == 2) launch_decode_gate_up<4, 2>(a, s, e2);
+    else if (mt == 4) launch_decode_gate_up<4, 4>(a, s, e2);
+    else launch_decode_gate_up<4, 8>(a, s, e2);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   // D3: down projections and the combine

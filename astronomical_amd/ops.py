@@ -484,6 +484,10 @@ class MoeBlock:
         if L.shared_intermediate:
             out["shared_out"] = get(v.shared_out, T * H, np.uint16).reshape(T, H)
             out["shared_gate_logits"] = get(v.shared_gate_logits, T, np.uint16)
+        if v.sorted_path and v.max_tiles:
+            n_tiles = int(get(v.tile_count, 1, np.uint32)[0])
+            out["tile_expert"] = get(v.tile_expert, v.max_tiles, np.uint32)[:n_tiles]
+            out["tile_row0"] = get(v.tile_row0, v.max_tiles, np.uint32)[:n_tiles]
         if L.slot_of_expert is not None:
             out["expert_slots"] = get(v.expert_slots, A, np.uint32).reshape(T, k)
             out["missing_slots"] = int(get(v.missing_slots, 1, np.uint32)[0])

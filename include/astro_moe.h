@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ASTRO_MOE_ABI_VERSION 4
+#define ASTRO_MOE_ABI_VERSION 5
 
 enum astro_moe_status {
   ASTRO_MOE_OK = 0,
@@ -119,6 +119,14 @@ typedef struct astro_moe_workspace_view {
   size_t shared_gate_logits; /* bf16 [T] */
   size_t expert_slots;       /* u32 [T][k] page slots (slot_of_expert set; else 0) */
   size_t missing_slots;      /* u32: routed experts absent from the page (slot_of_expert set) */
+  /* Sorted path only (0 on the decode path): the grouped GEMMs' tile table written by the
+   * sort -- u32 tile_expert[max_tiles], u32 tile_row0[max_tiles] (first sorted row of the
+   * tile), u32 tile_count (tiles in use).  Tiles hold up to 128 rows of one expert; every
+   * tile of more than 64 rows is listed before the smaller last tiles. */
+  size_t tile_expert;
+  size_t tile_row0;
+  size_t tile_count;
+  size_t max_tiles;          /* entries of tile_expert / tile_row0 (a count, not an offset) */
 } astro_moe_workspace_view;
 
 const char *astro_moe_last_error(void);

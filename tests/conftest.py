@@ -19,7 +19,7 @@ def pytest_configure(config):
 def orc():
     import oracle
     oracle.lib()
-    oracle.set_threads(min(8, os.cpu_count() or 1))
+    oracle.set_threads(min(16, os.cpu_count() or 1))
     return oracle
 
 

@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported(L):
         assert hasattr(lib, n), n
     # and the binding declares exactly those
     assert sorted(L.EXPORTS) == names
-    assert lib.astro_moe_abi_version() == 4
+    assert lib.astro_moe_abi_version() == 5
 
 
 def test_invert_assignment_order_host_entry_point(L):
@@ -107,3 +107,26 @@ def test_workspace_too_small_carries_the_active_memory_marker(L):
     # geometry errors come before any device work
     s.top_k = 40
     assert lib.astro_moe_workspace_bytes(C.byref(s), 16, C.byref(need)) == L.INVALID_ARGUMENT
+
+
+def test_decoder_step_rejects_a_residual_output_aliasing_its_inputs(L):
+    """The fused decode step writes r while other workgroups still read the hidden states and
+    the attention output, so r may not overlap either (checked on the host, before any launch)."""
+    from astronomical_amd import configs as CF
+    from astronomical_amd import synthetic as S
+    from astronomical_amd.ops import layer_struct
+    import torch
+    Lw = S.make_layer(CF.C0)
+    Lt = Lw.map(lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16 if a.dtype == np.uint16 else np.int32)))
+    s = layer_struct(Lt)
+    lib = L.lib()
+    need = C.c_size_t()
+    T, H = 1, Lw.hidden
+    assert lib.astro_moe_decoder_ffn_workspace_bytes(C.byref(s), T, C.byref(need)) == 0
+    hidden, attn, out = 1 << 20, 1 << 24, 1 << 28  # fake addresses, never dereferenced
+    for r in (hidden, hidden + 64, attn, attn - 2 * T * H + 2):
+        rc = lib.astro_moe_decoder_ffn_forward(C.byref(s), C.c_void_p(hidden), C.c_void_p(attn), C.c_void_p(8),
+                                               1e-6, T, C.c_void_p(out), C.c_void_p(r), C.c_void_p(8),
+                                               need.value, None)
+        assert rc == L.INVALID_ARGUMENT, r
+        assert "residual output must not overlap" in lib.astro_moe_last_error().decode()

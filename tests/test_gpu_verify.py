@@ -174,3 +174,30 @@ def test_block_decode_below_the_sorted_threshold_is_token_local(ops, c1_block, T
     whole = _host(c1_block(ops._bf16_dev(x)))
     for t in range(T):
         assert np.array_equal(_host(c1_block(ops._bf16_dev(x[t:t + 1])))[0], whole[t]), f"token {t} of {T}"
+
+
+def test_block_verification_window_keeps_the_unsorted_combine_at_top_64(ops, orc):
+    """top_k = 64 leaves the decode kernels (k <= 8), so the window runs one token at a time
+    through the grouped-GEMM path with 64 assignments per token; the verification contract
+    (resident_execution.rs:146-208) still asks for the unsorted reduction there: the device's
+    sparse output equals the oracle's unsorted weighted sum of the device's own expert outputs
+    bit for bit, and y is within the FP bar of it."""
+    from moe_testutil import assert_bf16_close
+    cfg = CF.C0.with_(name="c0_k64", experts=128, top_k=64)
+    L = S.make_layer(cfg)
+    blk = ops.MoeBlock(ops.to_device(L))
+    x = S.make_tokens(cfg, 3)
+    ws = torch.empty(1 << 24, dtype=torch.uint8, device="cuda")
+    got = _host(blk.target_verification_forward(ops._bf16_dev(x), workspace=ws))
+    tr = blk.trace(1, workspace=ws)  # the last piece: token 2 alone
+    eo = tr["expert_out_sorted"][tr["inverse_order"]].reshape(1, 64, -1)
+    want_sparse = orc.unsorted_weighted_sum(eo, tr["scores"])
+    assert np.array_equal(tr["sparse"], want_sparse)
+    assert np.array_equal(got[2:3], want_sparse)
+    sorted_sparse = orc.sorted_weighted_sum(tr["expert_out_sorted"], tr["inverse_order"], tr["scores"])
+    assert not np.array_equal(sorted_sparse, want_sparse)  # the two roundings differ here
+    assert_bf16_close(got[2:3], orc.moe_block_forward(L, x[2:3], logits_override=tr["logits"]),
+                      "k=64 verification token")
+    for t in range(3):  # token-local: each row equals its one-token window
+        one = _host(blk.target_verification_forward(ops._bf16_dev(x[t:t + 1])))
+        assert np.array_equal(one[0], got[t]), t
