@@ -108,6 +108,8 @@ EXPORTS = {
     "astro_moe_workspace_layout": ([C.POINTER(Layer), C.c_int32, C.POINTER(WorkspaceView)], C.c_int),
     "astro_moe_block_forward": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
                                  C.c_size_t, C.c_void_p], C.c_int),
+    "astro_moe_block_forward_no_alloc": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p],
+                                         C.c_int),
     "astro_moe_block_forward_attributed": ([C.POINTER(Layer), C.c_void_p, C.c_int32, C.c_void_p,
                                             C.c_void_p, C.c_size_t, C.c_void_p,
                                             C.POINTER(C.c_float)], C.c_int),

@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -694,6 +695,59 @@ int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
 int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
                             uint16_t *y, void *workspace, size_t workspace_bytes, void *stream) {
   return run_block(layer, x, tokens, y, workspace, workspace_bytes, stream, nullptr);
+}
+
+}  // extern "C"
+
+// The no-allocation entry point's workspace: one static device array per GPU (each device
+// holds its own copy at its own address).  In host code `scratch` names a host-side stand-in,
+// not device memory: only the address hipGetSymbolAddress returns for the current device is
+// ever passed to a kernel.
+static __device__ __align__(256) char scratch[ASTRO_MOE_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices];  // per device, looked up on its first call
+
+int device_scratch(const char *op, void **ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(op, e);
+  if (dev < 0 || dev >= kMaxDevices) return fail(ASTRO_MOE_UNSUPPORTED, op, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(op, e);
+    if (!p) return fail(ASTRO_MOE_HIP_ERROR, op, "the static scratch array has no device address");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return ASTRO_MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int astro_moe_block_forward_no_alloc(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                                     uint16_t *y, void *stream) {
+  size_t need = 0;
+  int rc = astro_moe_workspace_bytes(layer, tokens, &need);
+  if (rc) return rc;
+  if (need > ASTRO_MOE_STATIC_SCRATCH_BYTES)
+    return fail(ASTRO_MOE_WORKSPACE_TOO_SMALL, kBlockOp,
+                "the no-allocation entry point's static scratch is too small for %d tokens: "
+                "ASTRONOMICAL_MLX_ACTIVE_MEMORY_LIMIT_EXCEEDED active_bytes=0 allocation_bytes=%zu "
+                "allowed_bytes=%zu",
+                (int)tokens, need, (size_t)ASTRO_MOE_STATIC_SCRATCH_BYTES);
+  if (tokens == 0) return ok();
+  void *ws = nullptr;
+  rc = device_scratch(kBlockOp, &ws);
+  if (rc) return rc;
+  return run_block(layer, x, tokens, y, ws, ASTRO_MOE_STATIC_SCRATCH_BYTES, stream, nullptr);
 }
 
 // forward_moe_resident_target_verification (resident_execution.rs:146-208): the rows of an MTP

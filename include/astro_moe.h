@@ -148,6 +148,21 @@ int astro_moe_block_forward(const astro_moe_layer *layer, const uint16_t *x, int
                             void *stream);
 
 /*
+ * astro_moe_block_forward without a workspace argument and without any allocation: no
+ * counterpart in the reference.  It is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * block's intermediates live in a static device array of ASTRO_MOE_STATIC_SCRATCH_BYTES per
+ * GPU, held from the first call on that GPU until the process ends; a call whose workspace
+ * (astro_moe_workspace_bytes) exceeds it fails with ASTRO_MOE_WORKSPACE_TOO_SMALL.  Every
+ * call on one GPU shares that array: calls that overlap on one GPU (two streams, two host
+ * threads) race, so serialise them.  The first call on a device must not happen during
+ * graph capture (it looks up the array's address once per device).
+ */
+#define ASTRO_MOE_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
+int astro_moe_block_forward_no_alloc(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens,
+                                     uint16_t *y, void *stream);
+
+/*
  * The same forward with per-stage device times, the counterpart of the reference's
  * PerformanceAttribution operation timers (crates/model-serving/src/performance_attribution.rs:1-80,
  * performance_attribution/catalog.rs:54,89-91) — but measuring device time rather than
