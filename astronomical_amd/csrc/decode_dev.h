@@ -321,22 +321,31 @@ __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) 
 
 // ---------------------------------------------------------------- D2: route + gate/up
 
-// Routing of the <= 8 tokens from their logits (route_token), the stable sort of the <= 64
-// assignments and the table of distinct experts, into LDS; with publish, also written to the
-// workspace for the later kernels (ids, scores, sort, inverse, offsets, the table).
-template <int MT, int PER>
+// Routing of the <= 8 tokens from their logits, the stable sort of the <= 64 assignments and
+// the table of distinct experts, into LDS; with publish, also written to the workspace for the
+// later kernels (ids, scores, sort, inverse, offsets, the table).  EXACT: each token's slice in
+// the order of MLX's CPU argpartition (route_token_exact; waves 0 .. route_waves - 1 route, each
+// with kSelectWords<PER> words of sel_sh); otherwise the slice in ascending key order (route_token), which
+// gives the same set, hence the same distinct-expert table and rows per expert, but not the same
+// slot order -- enough for the gate/up GEMVs, not for anything published.
+template <int MT, int PER, bool EXACT>
 __device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, uint32_t *idx_sh, uint32_t *so_sh,
                                              uint32_t *sid_sh, uint32_t *key_sh, uint32_t (*route_sh)[kDecodeMaxK],
                                              uint16_t *sc_sh, uint32_t *g_expert_sh, uint32_t *g_start_sh,
-                                             uint32_t *g_count_sh, uint32_t &ng_sh) {
+                                             uint32_t *g_count_sh, uint32_t &ng_sh, uint32_t *sel_sh = nullptr,
+                                             int route_waves = 4) {
   constexpr int KM = kDecodeMaxK, AMAX = MT * KM;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
   const int A = p.A;
-  const int nwaves = (int)(blockDim.x >> 6);
-  for (int t = wave; t < p.T; t += nwaves) {
+  const int nwaves = EXACT ? route_waves : (int)(blockDim.x >> 6);
+  for (int t = wave; t < p.T && wave < nwaves; t += nwaves) {
     uint32_t my_idx, my_score;
-    route_token<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, route_sh[wave],
-                         my_idx, my_score);
+    if (EXACT) {
+      route_token_exact<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize,
+                                 sel_sh + wave * kSelectWords<PER>, route_sh[wave], my_idx, my_score);
+    } else {
+      route_token<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, route_sh[wave], my_idx, my_score);
+    }
     if (lane < p.k) {
       idx_sh[t * p.k + lane] = my_idx;
       sc_sh[t * p.k + lane] = (uint16_t)my_score;
@@ -408,25 +417,28 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, 
 template <int MT, int PER>
 __global__ __launch_bounds__(64 * MT) void decode_route_kernel(const DecodeArgs p) {
   constexpr int KM = kDecodeMaxK;
+  constexpr int RW = PER >= 16 ? 4 : MT;  // routing waves (LDS: kSelectWords<PER> words each)
   __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
   __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
   __shared__ __attribute__((aligned(16))) uint32_t route_sh[MT][KM];
   __shared__ uint16_t sc_sh[64];
   __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
-  decode_route<MT, PER>(p, true, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh,
-                        g_count_sh, ng_sh);
+  __shared__ uint32_t sel_sh[RW * kSelectWords<PER>];
+  decode_route<MT, PER, true>(p, true, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh,
+                              g_count_sh, ng_sh, sel_sh, RW);
 }
 
 // Workgroups (x, 0): the shared expert, which needs no routing — x < shared_pair_blocks
 // computes 4 (gate row, up row) pairs with the SwiGLU epilogue, x == shared_pair_blocks
 // the output gate z.  Workgroups (x, g + 1): rows of the gate/up GEMV of the g-th distinct
 // expert for every token routed to it (SwiGLU epilogue).  Without PRE (one token) every one
-// of them first recomputes the routing from the logits (route_token), the stable sort of the
-// assignments and the table of distinct experts — a few microseconds of one wave's work that
-// saves a dependent kernel boundary — and workgroup (0, 1) publishes them.  With PRE (batches
-// from kDecodeRouteOnceT tokens) decode_route_kernel has published the routing and the
-// workgroups read it instead.  RPW: (gate, up) row pairs per routed wave (more for larger
-// batches: fewer, fuller workgroups).
+// of them first recomputes the routing's set from the logits (route_token), the stable sort
+// of the assignments and the table of distinct experts — a few microseconds of one wave's work
+// that saves a dependent kernel boundary — and workgroup (shared_pair_blocks + 1, 0) computes
+// the routing in MLX's slot order (route_token_exact) and publishes it for the down kernel,
+// next to the GEMVs.  With PRE (batches from kDecodeRouteOnceT tokens) decode_route_kernel has
+// published the routing and the workgroups read it instead.  RPW: (gate, up) row pairs per
+// routed wave (more for larger batches: fewer, fuller workgroups).
 template <int BITS, int MT, int NC, int PER, bool PRE, int RPW>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
   constexpr int KM = kDecodeMaxK;
@@ -436,8 +448,14 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
   __shared__ uint16_t sc_sh[64];
   __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
   __shared__ int rows_sh[MT], orows_sh[MT];
+  __shared__ uint32_t sel_sh[PRE ? 1 : kSelectWords<PER>];  // the publisher's one routing wave
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int nchunks = p.H / 32;
+  if (!PRE && blockIdx.y == 0 && (int)blockIdx.x == p.shared_pair_blocks + 1) {
+    decode_route<MT, PER, true>(p, true, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh,
+                                g_count_sh, ng_sh, sel_sh, 1);
+    return;
+  }
   if (blockIdx.y == 0) {
     if (threadIdx.x < MT) {
       const int t = threadIdx.x < p.T ? threadIdx.x : p.T - 1;
@@ -490,8 +508,8 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
       orows_sh[threadIdx.x] = (int)(start + i);
     }
   } else {
-    decode_route<MT, PER>(p, blockIdx.x == 0 && blockIdx.y == 1, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh,
-                          g_expert_sh, g_start_sh, g_count_sh, ng_sh);
+    decode_route<MT, PER, false>(p, false, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh,
+                                 g_start_sh, g_count_sh, ng_sh);
     const int g = blockIdx.y - 1;
     if (g >= (int)ng_sh) return;
     e = g_expert_sh[g];
@@ -649,7 +667,9 @@ template <int BITS, int MT, int NC, int PER, int RPW>
 void launch_gate_up_rpw(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   // x: routed row blocks, or the shared expert's pair blocks and its output-gate block
   const int routed_x = (a.I + 4 * RPW - 1) / (4 * RPW);
-  const int shared_x = a.Is > 0 ? a.shared_pair_blocks + 1 : 0;
+  // x <= shared_pair_blocks: the shared expert; shared_pair_blocks + 1: the routing publisher
+  // (one token)
+  const int shared_x = a.T < kDecodeRouteOnceT ? a.shared_pair_blocks + 2 : a.Is > 0 ? a.shared_pair_blocks + 1 : 0;
   const dim3 grid(std::max(routed_x, shared_x), a.max_groups + 1);
   if (a.T >= kDecodeRouteOnceT)
     launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, true, RPW>, grid, s, ev, a);

@@ -8,18 +8,20 @@ namespace astro {
 
 namespace {
 
-// One wave per token (route_token in route_dev.h).
+// One wave per token (route_token_exact in route_dev.h: the slice in the order MLX's CPU
+// argpartition leaves it).
 template <int PER, int KMAX>
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restrict__ logits,
                                                          int T, int E, int k, int normalize,
                                                          uint32_t *__restrict__ idx,
                                                          uint16_t *__restrict__ scores) {
   __shared__ __attribute__((aligned(16))) uint32_t sh[4][KMAX];
+  __shared__ uint32_t sel[4][kSelectWords<PER>];  // per wave: keys, the partition's pair tables
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
   uint32_t my_idx, my_score;
-  route_token<PER, KMAX>(logits + (int64_t)t * E, E, k, normalize, sh[wave], my_idx, my_score);
+  route_token_exact<PER, KMAX>(logits + (int64_t)t * E, E, k, normalize, sel[wave], sh[wave], my_idx, my_score);
   if (lane < k) {
     idx[(int64_t)t * k + lane] = my_idx;
     scores[(int64_t)t * k + lane] = (uint16_t)my_score;

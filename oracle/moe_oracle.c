@@ -15,7 +15,10 @@
  *   orc_route_topk       reference KAT routing_and_combination.rs:12-68 ({3/7,4/7});
  *                        argpartition KAT numeric_operations.rs:268-300; invariants
  *                        (k distinct ids, every unselected p <= every selected p,
- *                        ties at the boundary go to the higher index); brute force
+ *                        ties at the boundary go to the higher index); brute force;
+ *                        slice order = libstdc++ std::nth_element with MLX's (value, index)
+ *                        comparator, called directly (orc_argpartition_bf16, argpartition.cc;
+ *                        tests/test_oracle_argpartition.py)
  *   orc_sort_assignments reference KATs routing_and_combination.rs:109-182 and
  *                        hermetic/sparse_experts.rs:5-36; numpy stable argsort
  *   orc_invert_assignment_order  hermetic/sparse_experts.rs:5-36 (values and errors)
@@ -45,8 +48,10 @@
  *                        ties to the lower id, softcap before sigmoid, normalisation) and
  *                        direct_mlx/laguna/routing.rs:63-122 ([0, 1] with bias); fp64 brute force
  * Reference choices that only an MLX build could pin (MLX 0.32.1 is not vendored):
- * the in-slice order of argpartition, MLX's CPU exp/sum order inside softmax, and its
- * accumulation order in quantized matmul.  The choices made here are stated at each
+ * MLX's CPU exp/sum order inside softmax and its accumulation order in quantized matmul.
+ * The in-slice order of argpartition is the C++ library's nth_element (called directly);
+ * that MLX's CPU argpartition calls std::nth_element with the (value, index) comparator
+ * is recalled from MLX's source, not pinned by a file here.  The choices made here are stated at each
  * function.
  */
 #include "moe_oracle.h"
@@ -180,11 +185,11 @@ void orc_router_logits(const uint16_t *x, const uint16_t *w, int32_t T, int32_t 
  * sums are combined by the butterfly lane[j] = lane[j] + lane[j ^ off] for
  * off = 1, 2, 4, 8, 16, 32 and S is lane 0.
  *
- * Selection: MLX's partition comparator orders (value, index) with index as the tie
- * break, so the selected set is the k largest (p, index) pairs — a tie at the
- * boundary goes to the higher expert index.  The order inside the selected slice is
- * unspecified by MLX; this restatement emits it ascending in (p, index), i.e. exactly
- * argsort(p)[E-k:].
+ * Selection: MLX's CPU argpartition runs std::nth_element over the index vector
+ * 0..E-1 with the comparator (value, index), so the selected set is the k largest
+ * (p, index) pairs — a tie at the boundary goes to the higher expert index — and the
+ * order inside the slice [E-k, E) is the one libstdc++'s introselect leaves
+ * (orc_argpartition_bf16, argpartition.cc, calls it).
  *
  * Renormalisation: sum in fp32 in slice order, rounded to bf16 (sum_axis output),
  * then bf16(s / sum) with IEEE division.
@@ -198,8 +203,8 @@ int orc_route_topk(const uint16_t *logits, int32_t T, int32_t E, int32_t k,
   {
     float *ex = (float *)malloc(sizeof(float) * (size_t)E);
     uint16_t *pb = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)E);
-    uint32_t *keys = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)E);
-    if (!ex || !pb || !keys) {
+    uint32_t *part = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)E);
+    if (!ex || !pb || !part) {
 #pragma omp atomic write
       err = ORC_ERR_GEOMETRY;
     } else {
@@ -223,23 +228,11 @@ int orc_route_topk(const uint16_t *logits, int32_t T, int32_t E, int32_t k,
         const float rcp = 1.0f / lane[0];
         for (int32_t i = 0; i < E; ++i) {
           pb[i] = tobf(ex[i] * rcp);
-          keys[i] = ((uint32_t)pb[i] << 16) | (uint32_t)i;
           if (probabilities) probabilities[(size_t)t * E + i] = pb[i];
         }
-        /* k largest keys, emitted ascending: slot k-1 holds the largest */
-        for (int32_t j = k - 1; j >= 0; --j) {
-          int32_t best = -1;
-          uint32_t bk = 0;
-          for (int32_t i = 0; i < E; ++i) {
-            if (keys[i] == 0xffffffffu) continue; /* already taken */
-            if (best < 0 || keys[i] > bk) {
-              best = i;
-              bk = keys[i];
-            }
-          }
-          indices[(size_t)t * k + j] = (uint32_t)best;
-          keys[best] = 0xffffffffu;
-        }
+        /* argpartition(p, E - k)[E - k:] */
+        orc_argpartition_bf16(pb, E, E - k, part);
+        for (int32_t j = 0; j < k; ++j) indices[(size_t)t * k + j] = part[E - k + j];
         uint16_t *s = scores + (size_t)t * k;
         const uint32_t *idx = indices + (size_t)t * k;
         for (int32_t j = 0; j < k; ++j) s[j] = pb[idx[j]];
@@ -253,7 +246,7 @@ int orc_route_topk(const uint16_t *logits, int32_t T, int32_t E, int32_t k,
     }
     free(ex);
     free(pb);
-    free(keys);
+    free(part);
   }
   return err;
 }

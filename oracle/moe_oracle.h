@@ -95,6 +95,11 @@ int orc_get_threads(void);
 /* stage functions (reference rows 1..12) */
 void orc_router_logits(const uint16_t *x, const uint16_t *w, int32_t T, int32_t H,
                        int32_t E, uint16_t *logits);
+/* MLX CPU argpartition (argpartition.cc): idx = 0..n-1 after std::nth_element at kth with the
+ * (value, index) comparator over bf16 values v. */
+void orc_argpartition_bf16(const uint16_t *v, int32_t n, int32_t kth, uint32_t *idx);
+/* a rank permutation that drives std::nth_element(n, kth) into its heap selection (test input) */
+void orc_adversarial_ranks(int32_t n, int32_t kth, int32_t *ranks);
 int orc_route_topk(const uint16_t *logits, int32_t T, int32_t E, int32_t k,
                    int32_t normalize, uint32_t *indices, uint16_t *scores,
                    uint16_t *probabilities);

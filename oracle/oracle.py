@@ -71,6 +71,10 @@ def lib():
         L.orc_get_threads.restype = C.c_int
         L.orc_router_logits.argtypes = [vp, vp, i32, i32, i32, vp]
         L.orc_route_topk.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp]
+        L.orc_argpartition_bf16.argtypes = [vp, i32, i32, vp]
+        L.orc_argpartition_bf16.restype = None
+        L.orc_adversarial_ranks.argtypes = [i32, i32, vp]
+        L.orc_adversarial_ranks.restype = None
         L.orc_sort_assignments.argtypes = [vp, i32, i32, vp, vp, vp, vp]
         L.orc_invert_assignment_order.argtypes = [vp, i32, vp]
         L.orc_dequantize.argtypes = [C.POINTER(_Affine), i32, vp]
@@ -149,6 +153,23 @@ def route_topk(logits, k, normalize=True, with_probabilities=False):
     _check(lib().orc_route_topk(_p(lg), T, E, k, int(bool(normalize)), _p(idx), _p(sc), _p(pr)),
            "route experts")
     return (idx, sc, pr) if with_probabilities else (idx, sc)
+
+
+def argpartition_bf16(values, kth):
+    """MLX CPU argpartition of one bf16 row: the index vector after libstdc++'s
+    std::nth_element at kth with the (value, index) comparator."""
+    v = _c(values, np.uint16).reshape(-1)
+    idx = np.empty(v.shape[0], np.uint32)
+    lib().orc_argpartition_bf16(_p(v), v.shape[0], int(kth), _p(idx))
+    return idx
+
+
+def adversarial_ranks(n, kth):
+    """A permutation of 0..n-1 that drives std::nth_element(kth) into its heap selection
+    (McIlroy's lazily-decided comparator; see argpartition.cc)."""
+    r = np.empty(n, np.int32)
+    lib().orc_adversarial_ranks(int(n), int(kth), _p(r))
+    return r
 
 
 def sort_assignments(ids, experts):

@@ -4,7 +4,9 @@
   (x; the weights are regenerated from the seeded generator and pinned by checksum) and
   the oracle's outputs of every stage.
 * route_ties.npz — router logits with exact ties at the top-k boundary (E=256 k=8 and
-  E=32 k=4) and the expected ids: the k largest (probability, index) keys, ascending.
+  E=32 k=4) and the expected ids: the slice of MLX's CPU argpartition of each row's
+  probabilities (oracle.argpartition_bf16, libstdc++'s std::nth_element with the (value,
+  index) comparator), i.e. the k largest (probability, index) keys in that order.
 
 Run: python tests/golden/make_fixtures.py   (needs the oracle library: make -C oracle)
 """
@@ -55,8 +57,7 @@ def make_ties():
             lg[t, order[k - span // 2:k + span // 2]] = lg[t, order[k - 1]]
         logits = f32_to_bf16(lg)
         _, _, p = oracle.route_topk(logits, k, True, with_probabilities=True)
-        keys = (p.astype(np.uint64) << np.uint64(16)) | np.arange(E, dtype=np.uint64)
-        expected = np.argsort(keys, axis=1, kind="stable")[:, E - k:].astype(np.uint32)
+        expected = np.stack([oracle.argpartition_bf16(row, E - k)[E - k:] for row in p]).astype(np.uint32)
         cases[f"logits_E{E}_k{k}"] = logits
         cases[f"indices_E{E}_k{k}"] = expected
     np.savez_compressed(os.path.join(HERE, "route_ties.npz"), **cases)

@@ -378,3 +378,36 @@ def test_device_generator_matches_numpy(ops):
         assert np.mean(_np(a) == b) > 0.9999
     xd = _np(DS.make_tokens_device(cfg, 16))
     assert np.mean(xd == S.make_tokens(cfg, 16)) > 0.9999
+
+
+def _adversarial_logits(orc, E, k):
+    """Logits whose probabilities order the experts as orc.adversarial_ranks does, so the
+    slice order comes out of libstdc++'s heap selection: the E largest-spaced bf16 values
+    in [-40, 0] whose softmax probabilities stay distinct in bf16."""
+    ranks = orc.adversarial_ranks(E, E - k)
+    cand = np.unique(f32_to_bf16(-np.linspace(0, 40, 40 * 64 + 1).astype(np.float32)))
+    vals = np.sort(bf16_to_f32(cand))[::-1]  # descending from 0
+    chosen, last_p = [], None
+    for v in vals:
+        p = np.float32(np.exp(np.float64(v)))
+        pb = f32_to_bf16(np.array([p], np.float32))[0]
+        if last_p is None or pb != last_p:
+            chosen.append(v)
+            last_p = pb
+        if len(chosen) == E:
+            break
+    levels = np.array(chosen[::-1], np.float32)  # ascending
+    return f32_to_bf16(levels[ranks])[None]
+
+
+@pytest.mark.parametrize("E,k", [(64, 4), (256, 8), (512, 16)])
+def test_route_topk_adversarial_rows_take_the_heap_selection(ops, orc, E, k):
+    from nth_element_model import nth_element
+    logits = _adversarial_logits(orc, E, k)
+    want_idx, want_sc, p = orc.route_topk(logits, k, True, with_probabilities=True)
+    keys = [(int(v), i) for i, v in enumerate(p[0])]
+    _, used_heap = nth_element(keys, E - k)
+    assert used_heap and len(set(p[0].tolist())) == E
+    idx, sc = ops.qwen3_5_moe_route_experts(_dev_bf16(logits), k, True)
+    assert np.array_equal(_np(idx), want_idx)
+    assert np.array_equal(_np(sc), want_sc)
