@@ -143,8 +143,10 @@ int expert_capacity(const astro_moe_layer &L) {
 bool decode_path(const astro_moe_layer &L, int T) {
   const int Is = L.shared_intermediate > 0 ? L.shared_intermediate : 0;
   const astro_moe_affine &gu = L.gate_up.w ? L.gate_up : L.gate;
+  const bool router_ok = L.router_w ? true
+                                    : (L.router_q.bits == 4 || L.router_q.bits == 8) && L.router_q.group_size >= 32;
   return !L.slot_of_expert && T >= 1 && T <= 8 && T * L.top_k <= 64 && L.top_k <= kDecodeMaxK &&
-         L.router_w != nullptr && L.hidden <= 4096 &&
+         router_ok && L.hidden <= 4096 &&
          L.intermediate <= 1024 && Is <= 1024 && (gu.bits == 4 || gu.bits == 8) &&
          (L.down.bits == 4 || L.down.bits == 8) &&
          (Is == 0 || L.shared_down.bits == L.down.bits);
@@ -291,7 +293,10 @@ hipError_t run_router(const astro_moe_layer &L, const uint16_t *x, int T, uint16
     set_weights(g, L.router_q, nullptr, 0);
   }
   g.bias = L.router_bias;
-  return launch_grouped_gemm(g, L.router_bias ? kEpiBias : kEpiPlain, s);
+  const int epi = L.router_bias ? kEpiBias : kEpiPlain;
+  // an affine router keeps its codes exact (the routing bits hang on the logits)
+  if (!L.router_w && affine_rows_supported(g, epi)) return launch_affine_rows(g, epi, s);
+  return launch_grouped_gemm(g, epi, s);
 }
 
 // shared expert problems: act = swiglu(gate(x), up(x)) (gu); out = down(act) (dn)
@@ -525,6 +530,15 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     d.x = x;
     d.router_w = L.router_w;
     d.router_bias = L.router_bias;
+    if (!L.router_w) {
+      d.rq_w = L.router_q.w;
+      d.rq_s = L.router_q.scales;
+      d.rq_b = L.router_q.biases;
+      d.rq_bits = L.router_q.bits;
+      d.rq_group = L.router_q.group_size;
+      d.rq_w_rs = words_per_row(L.router_q);
+      d.rq_sb_rs = groups_per_row(L.router_q);
+    }
     const astro_moe_affine &g = L.gate_up.w ? L.gate_up : L.gate;
     const astro_moe_affine &u = L.gate_up.w ? L.gate_up : L.up;
     const int64_t up_off = L.gate_up.w ? (int64_t)I : 0;

@@ -17,7 +17,9 @@
 namespace astro {
 
 bool decode_supported(const DecodeArgs &a) {
-  return a.T >= 1 && a.T <= 8 && a.A <= 64 && a.router_w != nullptr && a.H % 32 == 0 &&
+  const bool router_ok = a.router_w ? !a.rq_w
+                                    : a.rq_w && (a.rq_bits == 4 || a.rq_bits == 8) && a.rq_group >= 32;
+  return a.T >= 1 && a.T <= 8 && a.A <= 64 && router_ok && a.H % 32 == 0 &&
          a.H <= 4096 && a.I % 32 == 0 && a.I <= 1024 && a.Is % 32 == 0 && a.Is <= 1024 &&
          a.E <= 1024 && a.k >= 1 && a.k <= kDecodeMaxK && (a.gu_bits == 4 || a.gu_bits == 8) &&
          (a.dn_bits == 4 || a.dn_bits == 8) && a.gu_group >= 32 && a.dn_group >= 32 &&

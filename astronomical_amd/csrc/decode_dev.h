@@ -234,11 +234,13 @@ __device__ __forceinline__ void rows_task_q(const uint32_t *gw, const uint16_t *
 
 // ---------------------------------------------------------------- D1: router
 
-// Router GEMV: one wave per expert row (bf16 weights), every token.  STEP (the decoder step):
-// every workgroup first forms r = bf16(h + a) and the RMS-normalised rows n of the T tokens in
-// LDS (the order of add_rms_norm_kernel: rms_* in common.h) and reads its activations from
-// there; workgroup 0 also writes r and n for the later kernels.
-template <int MT, int NC, bool STEP>
+// Router GEMV: one wave per expert row, every token.  QB = 0: bf16 weights (forward.rs:59-91,
+// matmul); QB = 4 or 8: an affine router (forward.rs:53-58, quantized_linear), its rows
+// dequantised per 32-input chunk as the gate/up GEMVs do (chunk_dot).  STEP (the decoder
+// step): every workgroup first forms r = bf16(h + a) and the RMS-normalised rows n of the T
+// tokens in LDS (the order of add_rms_norm_kernel: rms_* in common.h) and reads its
+// activations from there; workgroup 0 also writes r and n for the later kernels.
+template <int MT, int NC, bool STEP, int QB>
 __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // STEP: n, [T][H]
   __shared__ float wsum[4];
@@ -277,12 +279,37 @@ __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) 
   }
   if (e >= p.E) return;
   const int nchunks = p.H / 32;
-  const uint16_t *w = p.router_w + (int64_t)e * p.H;
   float acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+  if constexpr (QB != 0) {
+    const uint32_t *wr = p.rq_w + (int64_t)e * p.rq_w_rs;
+    const uint16_t *sr = p.rq_s + (int64_t)e * p.rq_sb_rs, *br = p.rq_b + (int64_t)e * p.rq_sb_rs;
 #pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
+    for (int cc = 0; cc < NC; ++cc) {
+      const int craw = lane + 64 * cc;
+      const bool cv = craw < nchunks;
+      const int c = cv ? craw : 0;
+      WChunk wc;
+      load_wchunk<QB>(wc, wr, sr, br, c, p.rq_group);
+      XRaw xr[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int tr = t < p.T ? t : p.T - 1;
+        load_xraw(xr[t], (STEP ? xs : p.x) + (int64_t)tr * p.H + c * 32);
+      }
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        XChunk xc;
+        convert_xchunk<QB>(xc, xr[t]);
+        const float d = chunk_dot<QB>(wc, xc);
+        acc[t] += cv ? d : 0.0f;
+      }
+    }
+  }
+#pragma unroll
+  for (int cc = 0; cc < (QB == 0 ? NC : 0); ++cc) {
+    const uint16_t *w = p.router_w + (int64_t)e * p.H;
     const int craw = lane + 64 * cc;
     const bool cv = craw < nchunks;
     const int c = cv ? craw : 0;
@@ -740,27 +767,34 @@ void launch_down(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   else launch_down_nc<BITS, 2>(a, s, ev);
 }
 
-template <int MT, int NC>
+template <int MT, int NC, int QB>
 void launch_router_nc(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
   if (!a.norm_w) {
     // one wave per workgroup: the E rows' loads come from E CUs rather than E / 4
     if (ev)
-      hipExtLaunchKernelGGL(decode_router_kernel<MT, NC, false>, dim3(a.E), dim3(64), 0, s, ev[0], ev[1], 0, a);
+      hipExtLaunchKernelGGL(decode_router_kernel<MT, NC, false, QB>, dim3(a.E), dim3(64), 0, s, ev[0], ev[1], 0, a);
     else
-      hipLaunchKernelGGL((decode_router_kernel<MT, NC, false>), dim3(a.E), dim3(64), 0, s, a);
+      hipLaunchKernelGGL((decode_router_kernel<MT, NC, false, QB>), dim3(a.E), dim3(64), 0, s, a);
     return;
   }
   const size_t lds = (size_t)a.T * a.H * 2;
   if (ev)
-    hipExtLaunchKernelGGL(decode_router_kernel<MT, NC, true>, dim3(blocks), dim3(256), lds, s, ev[0], ev[1], 0, a);
+    hipExtLaunchKernelGGL(decode_router_kernel<MT, NC, true, QB>, dim3(blocks), dim3(256), lds, s, ev[0], ev[1], 0, a);
   else
-    hipLaunchKernelGGL((decode_router_kernel<MT, NC, true>), dim3(blocks), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((decode_router_kernel<MT, NC, true, QB>), dim3(blocks), dim3(256), lds, s, a);
+}
+
+template <int MT, int QB>
+void launch_router_q(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
+  if (a.H <= 2048) launch_router_nc<MT, 1, QB>(a, blocks, s, ev);
+  else launch_router_nc<MT, 2, QB>(a, blocks, s, ev);
 }
 
 template <int MT>
 void launch_router(const DecodeArgs &a, int blocks, hipStream_t s, const hipEvent_t *ev) {
-  if (a.H <= 2048) launch_router_nc<MT, 1>(a, blocks, s, ev);
-  else launch_router_nc<MT, 2>(a, blocks, s, ev);
+  if (a.router_w) launch_router_q<MT, 0>(a, blocks, s, ev);
+  else if (a.rq_bits == 8) launch_router_q<MT, 8>(a, blocks, s, ev);
+  else launch_router_q<MT, 4>(a, blocks, s, ev);
 }
 
 }  // namespace

@@ -812,6 +812,165 @@ hipError_t launch_dense(const GemmArgs &a, int epi, hipStream_t s) {
   return launch(dense_gemm_kernel<kEpiPlain>, 1);
 }
 
+// ---------------------------------------------------------------- affine rows, exact codes
+//
+// Affine weights over one implicit group of rows with the codes exact on the MFMA (the router
+// projection of an affine router, quantized_linear, forward.rs:53-58, at prefill sizes).  A
+// 32-input MFMA step never crosses an affine group (g >= 32), so each group's sum is
+//   sum_k x (s q + b) = s * sum_k x (MAG + q) + (b - MAG s) * sum_k x,
+// with MAG + q made exact in bf16 by OR-ing the 4-bit code into the mantissa of 128 (8-bit
+// codes convert exactly, MAG = 0) and sum_k x from an MFMA against ones; the affine terms are
+// applied to the group's fp32 partial sums once per group.  No weight is rounded to bf16 (the
+// grouped GEMMs round dequantised weights before their MFMAs), so the logits stay within about
+// one bf16 ulp of an fp32 dequantise-and-dot, as the decode kernels' router does.
+// Tile: 32 rows x 64 weight rows per 4-wave workgroup, K steps of 128 staged in LDS with the
+// next step's loads in registers during the current step's MFMAs; wave w owns weight rows
+// 16 w .. +16 of the tile and both 16-row blocks.
+constexpr int AQ_M = 32, AQ_N = 64, AQ_K = 128, AQ_J = AQ_K / 32;
+
+template <int BITS>
+__device__ __forceinline__ int aq_swz(int n) {  // 16-B piece XOR of weight row n (64 / 128-B rows)
+  return BITS == 4 ? ((n >> 2) & 3) : ((n >> 1) & 7);
+}
+
+template <int BITS, int EPI>
+__global__ __launch_bounds__(256) void affine_rows_gemm_kernel(const GemmArgs p, int nrb, int ncb) {
+  constexpr int BROW = AQ_K * BITS / 8;         // code bytes per weight row per step: 64 / 128
+  constexpr int BPC = BROW / 16;                // 16-B pieces per weight row
+  constexpr int BLD = AQ_N * BPC / 256;         // code pieces per thread per step: 1 / 2
+  constexpr float MAG = BITS == 4 ? 128.0f : 0.0f;
+  __shared__ __attribute__((aligned(16))) char As[AQ_M * AQ_K * 2];  // 256-B rows, chunk c at c ^ (r & 15)
+  __shared__ __attribute__((aligned(16))) char Bs[AQ_N * BROW];
+  __shared__ float Ss[AQ_N][AQ_J], Cs[AQ_N][AQ_J];  // s and b - MAG s of each 32-input step's group
+  const int blk = blockIdx.x;
+  const int rb = (blk & 7) + 8 * (blk / (8 * ncb));
+  const int cb = (blk >> 3) % ncb;
+  if (rb >= nrb) return;  // grid padding to whole rounds of 8 row blocks
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nk = p.K / AQ_K;
+  // this thread's loads of a step: two 16-B pieces of activations, BLD of codes, one (s, b)
+  const uint16_t *asrc[2];
+  int adst[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = tid + 256 * i, r = q >> 4, pc = q & 15;
+    const int gr = rb * AQ_M + r;
+    asrc[i] = p.A + (int64_t)(gr < p.M ? gr : p.M - 1) * p.lda + 8 * pc;
+    adst[i] = r * 256 + 16 * (pc ^ (r & 15));
+  }
+  const uint32_t *bsrc[BLD];
+  int bdst[BLD];
+#pragma unroll
+  for (int i = 0; i < BLD; ++i) {
+    const int q = tid + 256 * i, n = q / BPC, pc = q % BPC;
+    const int gn = cb * AQ_N + n;
+    bsrc[i] = p.w0 + (int64_t)(gn < p.N ? gn : p.N - 1) * p.w_row_stride + 4 * pc;
+    bdst[i] = n * BROW + 16 * (pc ^ aq_swz<BITS>(n));
+  }
+  const int sn = tid >> 2, sj = tid & 3;  // (weight row, 32-input step) of the (s, b) load
+  const int64_t sbo = (int64_t)(cb * AQ_N + sn < p.N ? cb * AQ_N + sn : p.N - 1) * p.sb_row_stride;
+  const uint16_t *srow = p.s0 + sbo, *brow = p.b0 + sbo;
+  u32x4 ra[2], rbq[BLD];
+  uint16_t rs, rbias;
+  auto load = [&](int k) {
+    const int k0 = k * AQ_K;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ra[i] = *(const u32x4 *)(asrc[i] + k0);
+#pragma unroll
+    for (int i = 0; i < BLD; ++i) rbq[i] = *(const u32x4 *)(bsrc[i] + k0 * BITS / 32);
+    const int gi = (k0 + 32 * sj) / p.group;
+    rs = srow[gi];
+    rbias = brow[gi];
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *(u32x4 *)(As + adst[i]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < BLD; ++i) *(u32x4 *)(Bs + bdst[i]) = rbq[i];
+    const float sv = bf2f(rs);
+    Ss[sn][sj] = sv;
+    Cs[sn][sj] = __builtin_fmaf(-MAG, sv, bf2f(rbias));
+  };
+  const int c16 = lane & 15, kq = lane >> 4;
+  const int n = wave * 16 + c16;  // this lane's weight row in the tile
+  const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[2] = {zero, zero}, part[2] = {zero, zero}, xs[2] = {zero, zero};
+  load(0);
+  store();
+  __syncthreads();
+  for (int k = 0; k < nk; ++k) {
+    if (k + 1 < nk) load(k + 1);
+#pragma unroll
+    for (int j = 0; j < AQ_J; ++j) {
+      u32x4 b;
+      if constexpr (BITS == 4) {
+        const uint32_t wd = *(const uint32_t *)(Bs + n * BROW + 16 * (j ^ aq_swz<4>(n)) + 4 * kq);
+        b[0] = (wd & 0x000f000fu) | 0x43004300u;  // inputs (8 kq + i, 8 kq + i + 4) as 128 + q
+        b[1] = ((wd >> 4) & 0x000f000fu) | 0x43004300u;
+        b[2] = ((wd >> 8) & 0x000f000fu) | 0x43004300u;
+        b[3] = ((wd >> 12) & 0x000f000fu) | 0x43004300u;
+      } else {
+        const uint2 raw = *(const uint2 *)(Bs + n * BROW + 16 * ((2 * j + (kq >> 1)) ^ aq_swz<8>(n)) + 8 * (kq & 1));
+        const uint32_t w2[2] = {raw.x, raw.y};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t v = w2[h];
+          b[2 * h] = pack_bf2_hw((float)(v & 255u), (float)((v >> 8) & 255u));
+          b[2 * h + 1] = pack_bf2_hw((float)((v >> 16) & 255u), (float)(v >> 24));
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = h * 16 + c16;
+        u32x4 a = *(const u32x4 *)(As + r * 256 + 16 * ((4 * j + kq) ^ (r & 15)));
+        if constexpr (BITS == 4) {  // (x0, x4), (x1, x5), (x2, x6), (x3, x7): the codes' pairing
+          const u32x4 d = a;
+          a[0] = (d[0] & 0xffffu) | (d[2] << 16);
+          a[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
+          a[2] = (d[1] & 0xffffu) | (d[3] << 16);
+          a[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
+        }
+        part[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                          part[h], 0, 0, 0);
+        xs[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, ones),
+                                                        xs[h], 0, 0, 0);
+      }
+      if ((k * AQ_K + 32 * (j + 1)) % p.group == 0) {  // the group ends with this step
+        const float sv = Ss[n][j], cv = Cs[n][j];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[h][i] = __builtin_fmaf(cv, xs[h][i], __builtin_fmaf(sv, part[h][i], acc[h][i]));
+          part[h] = zero;
+          xs[h] = zero;
+        }
+      }
+    }
+    __syncthreads();
+    if (k + 1 < nk) {
+      store();
+      __syncthreads();
+    }
+  }
+  // lane holds column c16 of rows 4 kq + i of each 16-row block
+  const int col = cb * AQ_N + n;
+  if (col >= p.N) return;
+  const float bias = EPI == kEpiBias ? bf2f(p.bias[col]) : 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb * AQ_M + h * 16 + kq * 4 + i;
+      if (r >= p.M) continue;
+      float v = acc[h][i];
+      if (EPI == kEpiBias) v = round_bf(v) + bias;
+      p.C[(int64_t)r * p.ldc + col] = (uint16_t)f2bf(v);
+    }
+  }
+}
+
 bool use_dense(const GemmArgs &a, int epi) {
   // one implicit group, bf16 weights, 16-B aligned 64-input steps, no row indirection
   return a.bkind == kBDense && !a.tile_expert && !a.a_rows && !a.c_rows && epi != kEpiSwiglu &&
@@ -828,6 +987,25 @@ bool use_ws(const GemmArgs &a) {
 }
 
 }  // namespace
+
+bool affine_rows_supported(const GemmArgs &a, int epilogue) {
+  return (a.bkind == kBQ4 || a.bkind == kBQ8) && !a.tile_expert && !a.a_rows && !a.a_rows2 && !a.c_rows &&
+         epilogue != kEpiSwiglu && a.K % AQ_K == 0 && a.group >= 32 && a.lda % 8 == 0 &&
+         a.w_row_stride % 4 == 0 && a.M > 0 && a.N > 0 && ((uintptr_t)a.A & 15) == 0 &&
+         ((uintptr_t)a.w0 & 15) == 0;
+}
+
+hipError_t launch_affine_rows(const GemmArgs &a, int epilogue, hipStream_t s) {
+  const int nrb = (a.M + AQ_M - 1) / AQ_M, ncb = (a.N + AQ_N - 1) / AQ_N;
+  const int grid = ((nrb + 7) & ~7) * ncb;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, s, a, nrb, ncb);
+    return hipGetLastError();
+  };
+  if (a.bkind == kBQ8)
+    return epilogue == kEpiBias ? go(affine_rows_gemm_kernel<8, kEpiBias>) : go(affine_rows_gemm_kernel<8, kEpiPlain>);
+  return epilogue == kEpiBias ? go(affine_rows_gemm_kernel<4, kEpiBias>) : go(affine_rows_gemm_kernel<4, kEpiPlain>);
+}
 
 hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s) {
   return launch_grouped_gemm2(a, nullptr, epilogue, s);

@@ -53,6 +53,11 @@ hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s);
 // tiles follow a's); problems the same kernel cannot serve are launched one after the other
 hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilogue, hipStream_t s);
 
+// Affine weights over one implicit group of rows with exact codes on the MFMA (no bf16
+// rounding of dequantised weights): the prefill router projection of an affine router.
+bool affine_rows_supported(const GemmArgs &a, int epilogue);
+hipError_t launch_affine_rows(const GemmArgs &a, int epilogue, hipStream_t s);
+
 hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
                              uint32_t *idx, uint16_t *scores, hipStream_t s);
 
@@ -117,6 +122,11 @@ hipError_t launch_combine_shared(const uint16_t *sparse, const uint16_t *shared_
 struct DecodeArgs {
   int T, A, H, E, k, I, Is, normalize;
   const uint16_t *x, *router_w, *router_bias;
+  // affine router (router_w null): codes [E][H * rq_bits / 32], scales / biases [E][H / rq_group]
+  const uint32_t *rq_w;
+  const uint16_t *rq_s, *rq_b;
+  int rq_bits, rq_group;
+  int64_t rq_w_rs, rq_sb_rs;
   // routed gate/up (fused or separate pages share strides) and down
   const uint32_t *gate_w, *up_w, *down_w;
   const uint16_t *gate_s, *gate_b, *up_s, *up_b, *down_s, *down_b;

@@ -106,13 +106,25 @@ def zipf_router_bias(cfg: LayerConfig, seed: int) -> np.ndarray:
     return f32_to_bf16(b.astype(np.float32))
 
 
+def router_config(cfg: LayerConfig, bits: int) -> LayerConfig:
+    """Distributions of an affine router (mlp.gate quantized, as the reference's certified
+    Qwen3.5/3.6-MoE checkpoints have it): group 64, codes uniform, biases centred as for the
+    experts; scales U[0.002, 0.02] at 4 bits and U[1e-4, 1e-3] at 8 bits, so the dequantised
+    weights have a standard deviation of a few hundredths, like the bf16 router's N(0, 0.02)."""
+    lo_hi = (0.002, 0.02) if bits == 4 else (1e-4, 1e-3)
+    return cfg.with_(bits=bits, group_size=64, scale_range=lo_hi, bias_noise=1e-3 if bits == 4 else 0.0)
+
+
 def make_layer(cfg: LayerConfig, layer: int = 0, fused_gate_up: bool = True,
-               keep_separate: bool = False) -> MoeLayerWeights:
-    """Weights of one synthetic layer as numpy arrays (host)."""
+               keep_separate: bool = False, router_bits: int | None = None) -> MoeLayerWeights:
+    """Weights of one synthetic layer as numpy arrays (host).  router_bits (4 or 8): an affine
+    router [1, E, H*bits/32] instead of the bf16 one."""
     s = cfg.seed
     p = f"L{layer}/"
     H, E, I, Is = cfg.hidden, cfg.experts, cfg.intermediate, cfg.shared_intermediate
-    router = f32_to_bf16((0.02 * normal(s, p + "router", (E, H))).astype(np.float32))
+    router = None
+    if router_bits is None:
+        router = f32_to_bf16((0.02 * normal(s, p + "router", (E, H))).astype(np.float32))
     gate = affine(cfg, s, p + "gate", E, I, H)
     up = affine(cfg, s, p + "up", E, I, H)
     down = affine(cfg, s, p + "down", E, H, I)
@@ -125,6 +137,8 @@ def make_layer(cfg: LayerConfig, layer: int = 0, fused_gate_up: bool = True,
     L = MoeLayerWeights(H, E, cfg.top_k, I, Is, cfg.normalize_top_k, router, gate_up, down,
                         gate=gate if (keep_separate or not fused_gate_up) else None,
                         up=up if (keep_separate or not fused_gate_up) else None)
+    if router_bits is not None:
+        L.router_q = affine(router_config(cfg, router_bits), s, p + f"router_q{router_bits}", 1, E, H)
     if cfg.zipf_s:
         L.router_bias = zipf_router_bias(cfg, s)
     if Is:

@@ -205,6 +205,7 @@ def main():
     if not args.no_extra:
         extra = decoder_step(CF, DS, ops, torch, blocks, K, W)
         extra["c1_decode_batched"] = batched_decode(CF, DS, ops, torch, blocks, K, W)
+        extra["c1_decode_affine_router"] = affine_router_decode(CF, DS, ops, torch, layers, K, W)
         extra.update(other_configs(CF, DS, ops, torch, K, W, layers[0]))
         extra["verification_lm_head"] = verification_qmv(CF, DS, ops, torch)
 
@@ -465,6 +466,54 @@ def batched_decode(CF, DS, ops, torch, blocks, K, W, sizes=(2, 4, 8)):
                         "achieved_GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         del g, x, y, ws
     log(f"batched decode: {json.dumps(out)}")
+    return out
+
+
+def affine_router_decode(CF, DS, ops, torch, layers, K, W, bits=4):
+    """c1 decode B=1 with an affine router (mlp.gate quantized to 4-bit g64, as the
+    reference's certified checkpoints have it) through a graph of the same layers' experts:
+    the decode kernels' quantized router row GEMV in place of the bf16 one."""
+    import copy
+    from astronomical_amd import synthetic as S
+    cfg = CF.C1
+    H, nL = cfg.hidden, len(layers)
+    rcfg = S.router_config(cfg, bits)
+    blocks = []
+    for l, L in enumerate(layers):
+        Lq = copy.copy(L)
+        Lq.router_w = None
+        Lq.router_q = DS.affine(rcfg, cfg.seed, f"L{l}/router_q{bits}", 1, cfg.experts, H)
+        blocks.append(ops.MoeBlock(Lq))
+    x = DS.make_tokens_device(cfg, nL, step=13).reshape(nL, 1, H)
+    y = torch.empty_like(x)
+    ws = torch.empty(blocks[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+
+    def step():
+        for l in range(nL):
+            blocks[l].forward(x[l], out=y[l], workspace=ws)
+    step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(W):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(K):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / K / nL * 1000
+    credited = (cfg.top_k + 1) * cfg.page_bytes
+    gbs = credited / (us * 1e-6) / 1e9
+    out = {"workload": f"c1 decode B=1, {bits}-bit g64 affine router, graph of {nL} layers",
+           "us_per_layer": round(us, 2), "tokens_per_s": round(1e6 / us, 1),
+           "achieved_GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "router_bytes_per_layer": int(cfg.experts * H * (bits / 8 + 4 / 64))}
+    log(f"affine-router decode: {json.dumps(out)}")
+    del blocks, g, x, y, ws
     return out
 
 

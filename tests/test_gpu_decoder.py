@@ -32,9 +32,12 @@ def test_add_rms_norm_bit_exact(orc, T, H, with_attn):
     assert np.array_equal(ops.bf16_to_numpy(n), n_ref)
 
 
-@pytest.mark.parametrize("cfg,T", [(CF.C0, 16), (CF.C1, 1), (CF.C1, 8), (CF.C0, 40)])
-def test_decoder_ffn_forward(orc, cfg, T):
-    L = S.make_layer(cfg)
+@pytest.mark.parametrize("cfg,T,router_bits", [(CF.C0, 16, None), (CF.C1, 1, None), (CF.C1, 8, None),
+                                               (CF.C0, 40, None), (CF.C1, 1, 4), (CF.C1, 4, 8)])
+def test_decoder_ffn_forward(orc, cfg, T, router_bits):
+    """The fused decode step (the router kernel forms r and n itself) also with an affine
+    router."""
+    L = S.make_layer(cfg, router_bits=router_bits)
     rng = np.random.default_rng(T)
     h = _bf(rng.standard_normal((T, cfg.hidden)))
     a = _bf(rng.standard_normal((T, cfg.hidden)) * 0.5)

@@ -59,6 +59,14 @@ def test_block_c2_full(ops, orc):
     print("c2 full", stats)
 
 
+def test_block_c2_full_affine_router(ops, orc):
+    """c2 with a 4-bit affine router (the certified checkpoints' quantized mlp.gate): the
+    router projection runs on the grouped GEMM."""
+    L = S.make_layer(CF.C1, router_bits=4)
+    stats = _check_block(ops, orc, L, S.make_tokens(CF.C2, 2048), "c2 T=2048 affine router")
+    print("c2 full affine router", stats)
+
+
 def test_block_c3_full(ops, orc):
     L = S.make_layer(CF.C3)
     T = 4096

@@ -251,7 +251,26 @@ def _check_block(ops, orc, L, x, what):
     y = _np(blk(_dev_bf16(x)))
     tr = blk.trace(T)
     # router projection: fp32 accumulation in another order -> within one bf16 ulp
-    want_logits = orc.router_logits(x, L.router_w) if L.router_bias is None else None
+    want_logits = None
+    if L.router_bias is None and L.router_q is not None:
+        # affine router: the decode kernels (T <= 8) and the prefill router GEMM both keep the
+        # codes exact and factor each group's terms as s * sum((MAG + q) x) + (b - MAG s) *
+        # sum(x) in fp32 -> bounded by the magnitudes those terms carry
+        want_logits = orc.qmm(x, L.router_q)
+        rq = L.router_q
+        deq = bf16_to_f32(orc.dequantize(rq)).astype(np.float64)
+        g = rq.group_size
+        sc = np.repeat(bf16_to_f32(rq.scales[0]).astype(np.float64), g, axis=1)
+        xf = bf16_to_f32(x).astype(np.float64)
+        mag = np.abs(xf) @ (np.abs(deq) + (1 << rq.bits) * sc).T
+        ref = bf16_to_f32(want_logits).astype(np.float64)
+        got = bf16_to_f32(tr["logits"]).astype(np.float64)
+        ulp = np.abs(np.spacing(ref.astype(np.float32)).astype(np.float64)) * 2 ** 16
+        assert np.all(np.abs(got - ref) <= ulp + 2.0 ** -16 * mag), what
+        assert np.mean(ulp_distance(tr["logits"], want_logits) <= 1) > 0.99, what
+        want_logits = None
+    elif L.router_bias is None:
+        want_logits = orc.router_logits(x, L.router_w)
     if want_logits is not None:
         # two fp32 accumulation orders differ by a few 2^-24 * sum|x*w| (absolute), then
         # each result is rounded to bf16: |diff| <= ulp(ref) + 2^-18 * sum|x*w|
@@ -318,6 +337,21 @@ def c1_layer():
 @pytest.mark.parametrize("T", [1, 2, 4, 8])
 def test_block_c1_decode(ops, orc, c1_layer, T):
     _check_block(ops, orc, c1_layer, S.make_tokens(CF.C1, T), f"c1 B={T}")
+
+
+@pytest.fixture(scope="module")
+def c1_affine_router_layers():
+    return {bits: S.make_layer(CF.C1, router_bits=bits) for bits in (4, 8)}
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("T", [1, 2, 4, 8, 64])
+def test_block_c1_affine_router(ops, orc, c1_affine_router_layers, bits, T):
+    """The reference's certified Qwen3.5/3.6-MoE checkpoints quantize mlp.gate
+    (tests/common/qwen3_5_moe.rs:299-308): the router runs as quantized_linear
+    (forward.rs:53-58).  T <= 8 takes the decode kernels' affine router, T = 64 the grouped
+    GEMM."""
+    _check_block(ops, orc, c1_affine_router_layers[bits], S.make_tokens(CF.C1, T), f"c1 affine router {bits}-bit T={T}")
 
 
 def test_block_c2_prefill_subset(ops, orc, c1_layer):
