@@ -17,22 +17,16 @@ using namespace astro;
 
 namespace {
 
-thread_local std::string g_last_error;
-
+int fail(int status, const char *op, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
 int fail(int status, const char *op, const char *fmt, ...) {
-  char buf[512];
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
+  const int r = vreport(status, op, fmt, ap);
   va_end(ap);
-  g_last_error = std::string(op) + ": " + buf;
-  return status;
+  return r;
 }
 
-int ok() {
-  g_last_error.clear();
-  return ASTRO_MOE_OK;
-}
+int ok() { return report_ok(); }
 
 int hip_fail(const char *op, hipError_t e) {
   return fail(ASTRO_MOE_HIP_ERROR, op, "HIP error %d (%s)", (int)e, hipGetErrorString(e));
@@ -49,17 +43,6 @@ int workspace_fail(const char *op, size_t need, size_t have) {
 
 }  // namespace
 
-int astro::report(int status, const char *op, const char *fmt, ...) {
-  char buf[768];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  g_last_error = std::string(op) + ": " + buf;
-  return status;
-}
-
-int astro::report_ok() { return ok(); }
 
 namespace {
 
@@ -126,7 +109,7 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 struct Layout {
   size_t logits, idx, scores, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
       tile_count, act, eout, sparse, shared_act, shared_out, z, groups, sort_scratch, slots, missing,
-      total;
+      xsum_x, xsum_act, xsum_sact, xpair, total;
   int max_tiles;
   bool decode;     // wavefront-GEMV path: act / eout hold A routed rows then T shared rows
   int64_t act_ld;  // row length of act
@@ -198,6 +181,12 @@ Layout block_layout(const astro_moe_layer &L, int T, int kk, bool with_router) {
     o.z = take(Is ? (size_t)T * 2 : 0);
     o.slots = take(with_router && L.slot_of_expert ? A * 4 : 0);
     o.missing = take(with_router && L.slot_of_expert ? 4 : 0);
+    // fp32 group sums of x, of the activated rows and of the shared expert's activated rows
+    // (the exact-code GEMMs' affine terms), sized for groups of 32
+    o.xsum_x = take((size_t)T * (L.hidden / 32) * 4);
+    o.xpair = take((size_t)T * L.hidden * 2);
+    o.xsum_act = take(A * (size_t)(L.intermediate / 32) * 4);
+    o.xsum_sact = take((size_t)T * (Is / 32) * 4);
   }
   o.total = p;
   return o;
@@ -396,6 +385,12 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
                              tile_count, (uint32_t *)at(o.sort_scratch), s);
   end(2);
   if (e != hipSuccess) return e;
+  // 4-bit projections run with exact codes on the group sums of their activation rows
+  const astro_moe_affine &gu_w = L.gate_up.w ? L.gate_up : L.gate;
+  float *xs_x = (float *)at(o.xsum_x), *xs_act = (float *)at(o.xsum_act), *xs_sact = (float *)at(o.xsum_sact);
+  const bool xq_gu = gu_w.bits == 4, xq_dn = L.down.bits == 4;
+  const bool xq_sgu = has_shared && L.shared_gate.bits == 4 && L.shared_gate.group_size == gu_w.group_size;
+  const bool xq_sdn = has_shared && L.shared_down.bits == 4;
 
   // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / kk]
   GemmArgs gu{};
@@ -421,9 +416,22 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
   if (has_shared)
     shared_gemm_args(L, x, T, (uint16_t *)at(o.shared_act), shared_out, sgu, sdn);
   begin(3);
+  // x's group sums and its copy in the codes' pairing, for the exact-code gate/up
+  uint16_t *xpair = (uint16_t *)at(o.xpair);
+  if (xq_gu || xq_sgu) e = launch_group_sums(x, H, T, H, gu_w.group_size, xs_x, H / gu_w.group_size, xpair, s);
+  auto paired_x = [&](GemmArgs &g) {
+    g.xsum = xs_x;
+    g.xsum_ld = H / gu_w.group_size;
+    g.A = xpair;
+    g.lda = H;
+    g.a_paired = 1;
+  };
+  if (xq_gu) paired_x(gu);
+  if (xq_sgu) paired_x(sgu);
   // the shared expert's tiles (whole 128-row tiles) first: the dispatcher deals workgroups in
   // order, so the lighter routed tiles fill the last, partial round of the grid
-  e = has_shared ? launch_grouped_gemm2(sgu, &gu, kEpiSwiglu, s) : launch_grouped_gemm2(gu, nullptr, kEpiSwiglu, s);
+  if (e == hipSuccess)
+    e = has_shared ? launch_grouped_gemm2(sgu, &gu, kEpiSwiglu, s) : launch_grouped_gemm2(gu, nullptr, kEpiSwiglu, s);
   end(3);
 
   GemmArgs dn{};
@@ -441,6 +449,17 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
   dn.C = eout;
   dn.ldc = H;
   begin(4);
+  if (e == hipSuccess && xq_dn) {
+    e = launch_group_sums(act, I, A, I, L.down.group_size, xs_act, I / L.down.group_size, nullptr, s);
+    dn.xsum = xs_act;
+    dn.xsum_ld = I / L.down.group_size;
+  }
+  if (e == hipSuccess && xq_sdn) {
+    const int Is = L.shared_intermediate, gs = L.shared_down.group_size;
+    e = launch_group_sums((const uint16_t *)at(o.shared_act), Is, T, Is, gs, xs_sact, Is / gs, nullptr, s);
+    sdn.xsum = xs_sact;
+    sdn.xsum_ld = Is / gs;
+  }
   if (e == hipSuccess)
     e = has_shared ? launch_grouped_gemm2(sdn, &dn, kEpiPlain, s) : launch_grouped_gemm2(dn, nullptr, kEpiPlain, s);
   end(4);
@@ -663,8 +682,6 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
 }  // namespace
 
 extern "C" {
-
-const char *astro_moe_last_error(void) { return g_last_error.c_str(); }
 
 int astro_moe_abi_version(void) { return ASTRO_MOE_ABI_VERSION; }
 

@@ -13,6 +13,7 @@
 // beyond the expert's rows are skipped, so ragged experts cost at most 15 wasted rows.
 // The next K step's global loads are issued before the MFMAs of the current one.
 #include "common.h"
+#include "gemm_dev.h"
 #include "kernels.h"
 
 #include <algorithm>
@@ -22,7 +23,6 @@ namespace astro {
 
 namespace {
 
-constexpr int BM = kGemmBM;  // rows per tile
 constexpr int BR = 128;      // weight rows per tile
 constexpr int BK = 64;       // K step
 constexpr int LDSP = BK + 8; // padded LDS row (bf16 elements); 144 B keeps 16 B alignment
@@ -111,39 +111,6 @@ __device__ __forceinline__ void store_b(uint16_t *dst, const BRegs &r, bool vali
   d[3] = out[3];
 }
 
-// Workgroup -> (row tile, column tile).  Workgroups are dealt to the 8 XCDs round-robin by
-// linear id (x fastest); the grid has a multiple of 8 row tiles.  Each XCD takes the row
-// tiles x = xcd (mod 8), and its column tiles of one row tile come one after the other in
-// its dispatch order, so they run together and share the activation tile in that XCD's L2.
-__device__ __forceinline__ void tile_of_block(int &bx, int &by) {
-  const int mt = (int)gridDim.x, nb = (int)gridDim.y;
-  const int l = (int)blockIdx.x + (int)blockIdx.y * mt;
-  const int xcd = l & 7, s = l >> 3;
-  bx = (s / nb) * 8 + xcd;
-  by = s - (s / nb) * nb;
-}
-
-// Tile of the launch: blocks x < split belong to problem a, the rest to problem b (a
-// second GEMM fused into the same launch, e.g. the shared expert next to the routed
-// experts).  A problem with a tile table is grouped: x indexes its tiles; otherwise row
-// tiles are consecutive.  Returns false when the block has no work.  The problem is
-// selected by value: taking the address of a kernel argument would copy both to scratch.
-__device__ __forceinline__ bool gemm_tile(const GemmArgs &p, int bx, int by, bool second, int split, int nblocks,
-                                          int &expert, int &row0, int &m_valid) {
-  if (by >= nblocks) return false;
-  const int x = second ? bx - split : bx;
-  expert = 0;
-  if (p.tile_expert) {
-    if (x >= (int)*p.tile_count) return false;
-    expert = (int)p.tile_expert[x];
-    row0 = (int)p.tile_row0[x];
-    m_valid = min(BM, (int)p.expert_offsets[expert + 1] - row0);
-  } else {
-    row0 = x * BM;
-    m_valid = min(BM, p.M - row0);
-  }
-  return m_valid > 0;
-}
 
 template <int KIND, int EPI>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(const GemmArgs pa, const GemmArgs pb,
@@ -348,36 +315,6 @@ hipError_t launch_kind(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_
   return hipGetLastError();
 }
 
-// Workgroup barrier without the memory fence of __syncthreads (whose release would wait for
-// every outstanding global->LDS load).  Each wave first waits for its own LDS accesses
-// (lgkmcnt 0), so its LDS stores are visible and its LDS reads are done when it reaches the
-// barrier; the async loads are covered by wait_vmcnt_le before it.  The asm statements
-// also stop the compiler from moving memory accesses across the barrier.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// s_waitcnt vmcnt(n) with expcnt and lgkmcnt at their maxima (no wait on them); n is a
-// compile-time constant at every call, so the switch folds to one instruction.
-__device__ __forceinline__ void wait_vmcnt_le(int n) {
-  switch (n) {
-#define ASTRO_WAITVM(N) \
-  case N:               \
-    __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | 0x0f70); \
-    break;
-#define ASTRO_WAITVM8(B) ASTRO_WAITVM(B) ASTRO_WAITVM(B + 1) ASTRO_WAITVM(B + 2) ASTRO_WAITVM(B + 3) \
-  ASTRO_WAITVM(B + 4) ASTRO_WAITVM(B + 5) ASTRO_WAITVM(B + 6) ASTRO_WAITVM(B + 7)
-    ASTRO_WAITVM8(0) ASTRO_WAITVM8(8) ASTRO_WAITVM8(16) ASTRO_WAITVM8(24)
-    ASTRO_WAITVM8(32) ASTRO_WAITVM8(40) ASTRO_WAITVM8(48) ASTRO_WAITVM8(56)
-#undef ASTRO_WAITVM8
-#undef ASTRO_WAITVM
-    default:
-      __builtin_amdgcn_s_waitcnt(0x0f70);
-      break;
-  }
-}
 
 // 4 words of codes (32 inputs, 4-bit, LSB first) -> 4 chunks of 8 bf16, the words'
 // conversions interleaved (each byte position converts 8 independent values) so that
@@ -1012,8 +949,10 @@ hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s) {
 }
 
 bool gemm_fusable(const GemmArgs &a, const GemmArgs &b) {
-  return a.bkind == b.bkind && use_ws(a) == use_ws(b);
+  return a.bkind == b.bkind && xq_supported(a) == xq_supported(b) && use_ws(a) == use_ws(b);
 }
+
+
 
 hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilogue, hipStream_t s) {
   if (b && !gemm_fusable(a, *b)) {
@@ -1021,6 +960,7 @@ hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilog
     return e == hipSuccess ? launch_grouped_gemm2(*b, nullptr, epilogue, s) : e;
   }
   if (!b && use_dense(a, epilogue)) return launch_dense(a, epilogue, s);
+  if (xq_supported(a)) return launch_xq(a, b, epilogue, s);
   if (use_ws(a)) return launch_ws(a, b, epilogue, s);
   switch (a.bkind) {
     case kBQ4: return launch_kind<kBQ4>(a, b, epilogue, s);

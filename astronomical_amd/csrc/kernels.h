@@ -8,7 +8,7 @@ namespace astro {
 
 // Rows of one grouped-GEMM tile; also the row granularity of the tile table the sort
 // kernels emit.
-constexpr int kGemmBM = 128;
+constexpr int kGemmBM = 64;
 
 enum BKind { kBQ4 = 0, kBQ8 = 1, kBDense = 2 };
 enum Epilogue { kEpiPlain = 0, kEpiSwiglu = 1, kEpiBias = 2 };
@@ -46,9 +46,21 @@ struct GemmArgs {
   uint16_t *C;
   int64_t ldc;
   const uint32_t *c_rows;  // sorted row -> destination row (nullptr: identity)
+  // optional fp32 group sums of the activation rows, xsum[src][gi] = sum of inputs gi * group ..
+  // + group of source row src (launch_group_sums): 4-bit weights then run with exact codes
+  const float *xsum;
+  int64_t xsum_ld;
+  int a_paired;  // the activation rows hold inputs (0, 4), (1, 5), (2, 6), (3, 7) of every 8
 };
 
 hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s);
+// the exact-code grouped GEMM for 4-bit weights (gemm_xq.hip): a.xsum set, shapes it serves
+bool xq_supported(const GemmArgs &a);
+hipError_t launch_xq(const GemmArgs &a, const GemmArgs *b, int epilogue, hipStream_t s);
+// X[r][gi] = fp32 sum of inputs gi * group .. + group of row r of A (rows x K bf16); paired
+// (nullable, rows x K): the rows with inputs (0, 4), (1, 5), (2, 6), (3, 7) of every 8 paired
+hipError_t launch_group_sums(const uint16_t *A, int64_t lda, int rows, int K, int group, float *X, int64_t ldx,
+                             uint16_t *paired, hipStream_t s);
 // a and, when b is non-null, a second problem b with the same epilogue in one launch (its
 // tiles follow a's); problems the same kernel cannot serve are launched one after the other
 hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilogue, hipStream_t s);

@@ -1,6 +1,7 @@
 // Expert pages from safetensors checkpoints: header parsing, the startup-validated layer plan,
 // the selected-page manifest and the bounded reader that writes exactly the selected experts'
-// bytes into host or HIP device buffers (host code; no kernel runs).
+// bytes into host or HIP device buffers.  Host code only (no kernel): it builds with the host
+// compiler, which is also how the sanitizer build of the host library takes it.
 //
 // Follows the reference's expert paging:
 //   parse_safetensors_header           expert_paging/safetensors_header.rs:171-276
@@ -13,7 +14,7 @@
 //   load_quantized_expert_page         expert_paging/bounded_expert_reader.rs:35-117
 //   resident gate/up fusion plan and concatenation
 //                                      qwen3_5_moe/expert_residency/resident_gate_up_fusion.rs:109-268
-#include <hip/hip_runtime.h>
+#include <hip/hip_runtime_api.h>
 
 #include <errno.h>
 #include <fcntl.h>
@@ -21,10 +22,12 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <set>
 #include <string>
 #include <utility>
 #include <vector>
@@ -62,11 +65,19 @@ struct Json {
   }
 };
 
+// The JSON the reference's serde_json reading accepts (serde_json 1.0.151 from_slice through
+// strict_json.rs:11-110): RFC 8259 with strings of valid UTF-8 (no raw control characters, no
+// lone surrogate escapes), numbers that are finite as f64, at most kMaxJsonNesting nested
+// arrays and objects (serde_json's recursion limit of 128), and no duplicate key in any object.
+// An integer literal is integral when it fits int64 (serde_json's as_i64); "-0" is not (serde_json
+// reads it as the float -0.0).
+constexpr int kMaxJsonNesting = 127;
+
 class JsonParser {
  public:
   JsonParser(const char *p, size_t n) : p_(p), end_(p + n) {}
 
-  // whole document: one value, then only whitespace; duplicate object keys are rejected
+  // whole document: one value, then only whitespace
   bool document(Json &out) {
     if (!value(out, 0)) return false;
     ws();
@@ -122,6 +133,22 @@ class JsonParser {
       const unsigned char c = (unsigned char)*p_++;
       if (c == '"') return true;
       if (c < 0x20) return false;
+      if (c >= 0x80) {  // one UTF-8 sequence, validated (no overlong form, surrogate or > U+10FFFF)
+        const int n = c >= 0xf0 ? 3 : c >= 0xe0 ? 2 : c >= 0xc2 ? 1 : -1;
+        if (n < 0 || c > 0xf4 || end_ - p_ < n) return false;
+        const unsigned char c1 = (unsigned char)p_[0];
+        if ((c1 & 0xc0) != 0x80) return false;
+        if (c == 0xe0 && c1 < 0xa0) return false;  // overlong 3-byte
+        if (c == 0xed && c1 >= 0xa0) return false;  // UTF-16 surrogate
+        if (c == 0xf0 && c1 < 0x90) return false;  // overlong 4-byte
+        if (c == 0xf4 && c1 >= 0x90) return false;  // above U+10FFFF
+        for (int i = 1; i < n; ++i)
+          if (((unsigned char)p_[i] & 0xc0) != 0x80) return false;
+        s += (char)c;
+        s.append(p_, (size_t)n);
+        p_ += n;
+        continue;
+      }
       if (c != '\\') {
         s += (char)c;
         continue;
@@ -182,7 +209,7 @@ class JsonParser {
     }
     out.kind = Json::Number;
     out.text.assign(b, p_);
-    if (integral) {
+    if (integral && out.text != "-0") {
       errno = 0;
       char *e = nullptr;
       const long long v = strtoll(out.text.c_str(), &e, 10);
@@ -191,13 +218,16 @@ class JsonParser {
         out.integer = v;
       }
     }
+    // a literal past f64's range is an error (an integer of any size still reads as a float)
+    if (!out.integral && std::isinf(strtod(out.text.c_str(), nullptr))) return false;
     return true;
   }
+  // depth: the arrays and objects this value is nested in
   bool value(Json &out, int depth) {
-    if (depth > 64) return false;
     ws();
     if (p_ >= end_) return false;
     const char c = *p_;
+    if ((c == '{' || c == '[') && depth >= kMaxJsonNesting) return false;
     if (c == '{') {
       ++p_;
       out.kind = Json::Object;
@@ -206,12 +236,12 @@ class JsonParser {
         ++p_;
         return true;
       }
+      std::set<std::string> keys;
       while (true) {
         ws();
         std::string key;
         if (!string(key)) return false;
-        for (const auto &m : out.members)
-          if (m.first == key) return false;  // duplicate entry
+        if (!keys.insert(key).second) return false;  // duplicate entry
         ws();
         if (p_ >= end_ || *p_ != ':') return false;
         ++p_;
@@ -387,10 +417,15 @@ int parse_header(const std::string &path, Header &h) {
   h.payload_start = 8 + n;
   h.file_size = size;
   const uint64_t payload = size - h.payload_start;
-  for (const auto &m : doc.members) {
-    const std::string &name = m.first;
+  // entries in key order (byte-wise), as the reference's map of them iterates: with several bad
+  // entries, the first by name is the one reported
+  std::vector<const std::pair<std::string, Json> *> entries;
+  for (const auto &m : doc.members) entries.push_back(&m);
+  std::sort(entries.begin(), entries.end(), [](const auto *x, const auto *y) { return x->first < y->first; });
+  for (const auto *m : entries) {
+    const std::string &name = m->first;
     if (name == "__metadata__") continue;
-    const Json &t = m.second;
+    const Json &t = m->second;
     if (t.kind != Json::Object)
       return report(ASTRO_MOE_INVALID_ARGUMENT, kHeaderOp, "safetensors header must be a JSON object, got %s",
                     json_text(t).c_str());
@@ -421,14 +456,17 @@ int parse_header(const std::string &path, Header &h) {
       return report(ASTRO_MOE_INVALID_ARGUMENT, kHeaderOp,
                     "tensor \"%s\" data_offsets are outside the file payload: [%llu, %llu) vs payload size %llu",
                     name.c_str(), (unsigned long long)s, (unsigned long long)en, (unsigned long long)payload);
-    unsigned __int128 count = kDtypeWidths[dtype];
-    for (int64_t d : e.shape) count *= (unsigned __int128)d;
-    if (count != (unsigned __int128)(en - s))
+    // element count with checked 64-bit products; an overflow reports 0 expected bytes
+    uint64_t count = 1;
+    bool overflow = false;
+    for (int64_t d : e.shape)
+      if (!overflow && __builtin_mul_overflow(count, (uint64_t)d, &count)) overflow = true;
+    const uint64_t expect = overflow ? 0 : count * (uint64_t)kDtypeWidths[dtype];
+    if (overflow || expect != en - s)
       return report(ASTRO_MOE_INVALID_ARGUMENT, kHeaderOp,
                     "tensor \"%s\" byte count mismatch: header declares %llu bytes but shape\xc3\x97"
                     "dtype expects %llu bytes",
-                    name.c_str(), (unsigned long long)(en - s),
-                    count >> 64 ? ~0ull : (unsigned long long)count);
+                    name.c_str(), (unsigned long long)(en - s), (unsigned long long)expect);
     e.start = h.payload_start + s;
     e.end = h.payload_start + en;
     h.tensors[name] = e;

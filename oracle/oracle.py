@@ -13,7 +13,8 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle_moe.so")
+# ASTRO_ORACLE_LIB names another build of the same sources (the sanitizer build of the tests)
+_LIB_PATH = os.environ.get("ASTRO_ORACLE_LIB") or os.path.join(_HERE, "liboracle_moe.so")
 
 ERRORS = {0: "ok", 1: "invalid geometry", 2: "unsupported", 3: "duplicate slot",
           4: "out-of-range slot", 5: "missing slot"}
@@ -60,6 +61,8 @@ def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(_LIB_PATH):
+            if os.environ.get("ASTRO_ORACLE_LIB"):
+                raise RuntimeError(f"ASTRO_ORACLE_LIB={_LIB_PATH} does not exist")
             build()
         L = C.CDLL(_LIB_PATH)
         vp, i32, i64 = C.c_void_p, C.c_int32, C.c_int64

@@ -1,9 +1,9 @@
 """The block at every configuration's stated size against the CPU oracle, on an MI355X.
 
-c2 (2048 tokens, near-uniform routing) puts 65-96 rows on about half of the experts, so its
-tiles run the 96-row consumer variant of the warp-specialised gate/up GEMM and the tile table
-lists its light last tiles after the heavy ones; c3 (4096 tokens, Zipf-skewed logits) puts
-every token on its top expert (32 whole tiles of one expert) and leaves most experts empty;
+c2 (2048 tokens, near-uniform routing) puts 65-96 rows on about half of the experts, so their
+rows span a full 64-row tile and a partial one, and the tile table lists the light last tiles
+after the heavy ones; c3 (4096 tokens, Zipf-skewed logits) puts
+every token on its top expert (64 whole tiles of one expert) and leaves most experts empty;
 c4 (512 tokens, 8-bit g32) runs the 8-bit grouped GEMMs at about 32 rows per expert, alone and
 as a two-layer residual chain (h <- h + MoE_l(rms_norm(h)), the decoder step of
 decoder_layer_forward.rs:111-174).  Bars as in test_gpu_parity: routing and permutation
@@ -26,19 +26,22 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
+TILE_ROWS = 64  # rows of a grouped-GEMM tile (kGemmBM)
+
+
 def _tile_checks(tr, what):
-    """The tile table covers every sorted row once, in tiles of at most 128 rows of one
-    expert, with every tile of more than 64 rows before the smaller last tiles."""
+    """The tile table covers every sorted row once, in tiles of at most 64 rows of one
+    expert, with every tile of more than 32 rows before the smaller last tiles."""
     off = tr["expert_offsets"].astype(np.int64)
     te, tr0 = tr["tile_expert"].astype(np.int64), tr["tile_row0"].astype(np.int64)
-    rows = np.minimum(128, off[te + 1] - tr0)
+    rows = np.minimum(TILE_ROWS, off[te + 1] - tr0)
     assert np.all(rows > 0), what
     covered = np.zeros(int(off[-1]), np.int32)
     for e, r0, n in zip(te, tr0, rows):
         assert off[e] <= r0 < off[e + 1], what
         covered[r0:r0 + n] += 1
     assert np.all(covered == 1), what
-    big = rows > 64
+    big = rows > TILE_ROWS // 2
     first_small = int(np.argmin(big)) if not big.all() else len(big)
     assert big[:first_small].all() and not big[first_small:].any(), what
     return rows
@@ -53,9 +56,10 @@ def test_block_c2_full(ops, orc):
     tr = blk.trace(T)
     rows = _tile_checks(tr, "c2 tiles")
     counts = np.diff(tr["expert_offsets"][:L.num_experts + 1].astype(np.int64))
-    # the 96-row consumer variant and the small-tail ordering are exercised
-    assert np.sum((counts > 64) & (counts <= 96)) >= 64, counts
-    assert np.sum((rows > 64) & (rows <= 96)) >= 64 and np.sum(rows <= 64) >= 64, rows
+    # experts of more than one tile, partial tiles of every size class, and small last tiles
+    # ordered after the heavy ones are all exercised
+    assert np.sum(counts > TILE_ROWS) >= 64, counts
+    assert np.sum(rows == TILE_ROWS) >= 64 and np.sum(rows <= TILE_ROWS // 2) >= 32, rows
     print("c2 full", stats)
 
 
