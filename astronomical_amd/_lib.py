@@ -49,7 +49,8 @@ class WorkspaceView(C.Structure):
         (n, C.c_size_t) for n in ("logits", "indices", "scores", "sorted_order", "inverse_order",
                                   "sorted_ids", "expert_offsets", "activated", "activated_ld", "expert_out",
                                   "sparse", "shared_out", "shared_gate_logits", "expert_slots",
-                                  "missing_slots", "tile_expert", "tile_row0", "tile_count", "max_tiles")]
+                                  "missing_slots", "tile_expert", "tile_row0", "tile_count", "max_tiles",
+                                  "activated_paired")]
 
 
 PATH_MAX = 1024

@@ -109,8 +109,8 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 struct Layout {
   size_t logits, idx, scores, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
       tile_count, act, eout, sparse, shared_act, shared_out, z, groups, sort_scratch, slots, missing,
-      xsum_x, xsum_act, xsum_sact, xpair, total;
-  int max_tiles;
+      xsum_x, xsum_act, xsum_sact, xpair, xtiles, total;
+  int max_tiles, max_xtiles;
   bool decode;     // wavefront-GEMV path: act / eout hold A routed rows then T shared rows
   int64_t act_ld;  // row length of act
 };
@@ -187,6 +187,9 @@ Layout block_layout(const astro_moe_layer &L, int T, int kk, bool with_router) {
     o.xpair = take((size_t)T * L.hidden * 2);
     o.xsum_act = take(A * (size_t)(L.intermediate / 32) * 4);
     o.xsum_sact = take((size_t)T * (Is / 32) * 4);
+    // the exact-code GEMMs' table of balanced tiles (launch_sort)
+    o.max_xtiles = sort_max_xtiles((int)A, (int)E);
+    o.xtiles = take((2 + 2 * (size_t)o.max_xtiles) * 4);
   }
   o.total = p;
   return o;
@@ -354,6 +357,99 @@ struct StageClock {
 // weighted sum -- sorted rounding iff A >= 64 (routing.rs:13) and not force_unsorted (an MTP
 // verification window).  with_shared: the shared expert's gate/up and down run in the routed
 // launches and y = the shared combine; otherwise y = the sparse output.
+// The GEMM problems of the sorted path: routed gate/up (SwiGLU) and down, and the shared
+// expert's, with the exact-code inputs decided: 4-bit gate/up reads x's copy in the codes'
+// pairing with its group sums (paired_x); its epilogue then writes the activated rows paired,
+// with their group sums, for an exact-code down projection (act_paired).  Neither happens when
+// the exact-code kernel cannot take the problem.
+struct SparsePlan {
+  GemmArgs gu{}, dn{}, sgu{}, sdn{};
+  bool has_shared = false;
+  bool paired_x = false;    // x's group sums and paired copy are needed
+  bool act_paired = false;  // the routed activated rows are stored in the codes' pairing
+};
+
+SparsePlan plan_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk, const Layout &o, char *ws,
+                       bool with_shared) {
+  auto at = [&](size_t off) { return (void *)(ws + off); };
+  SparsePlan P;
+  const int H = L.hidden, I = L.intermediate;
+  P.has_shared = with_shared && L.shared_intermediate > 0;
+  const astro_moe_affine &gu_w = L.gate_up.w ? L.gate_up : L.gate;
+  float *xs_x = (float *)at(o.xsum_x), *xs_act = (float *)at(o.xsum_act), *xs_sact = (float *)at(o.xsum_sact);
+  uint32_t *offsets = (uint32_t *)at(o.offsets);
+  // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / kk]
+  GemmArgs &gu = P.gu;
+  gu.A = x;
+  gu.lda = H;
+  gu.a_rows = (const uint32_t *)at(o.sorted_order);
+  gu.a_div = kk;
+  gu.K = H;
+  gu.N = I;
+  if (L.gate_up.w)
+    set_weights(gu, L.gate_up, &L.gate_up, I);
+  else
+    set_weights(gu, L.gate, &L.up, 0);
+  gu.tile_expert = (const uint32_t *)at(o.tile_expert);
+  gu.tile_row0 = (const uint32_t *)at(o.tile_row0);
+  gu.tile_count = (const uint32_t *)at(o.tile_count);
+  gu.expert_offsets = offsets;
+  gu.max_tiles = o.max_tiles;
+  gu.xtiles = (const uint32_t *)at(o.xtiles);
+  gu.max_xtiles = o.max_xtiles;
+  gu.C = (uint16_t *)at(o.act);
+  gu.ldc = I;
+  GemmArgs &dn = P.dn;
+  dn.A = (const uint16_t *)at(o.act);
+  dn.lda = I;
+  dn.a_div = 1;
+  dn.K = I;
+  dn.N = H;
+  set_weights(dn, L.down, nullptr, 0);
+  dn.tile_expert = gu.tile_expert;
+  dn.tile_row0 = gu.tile_row0;
+  dn.tile_count = gu.tile_count;
+  dn.expert_offsets = offsets;
+  dn.max_tiles = o.max_tiles;
+  dn.xtiles = gu.xtiles;
+  dn.max_xtiles = o.max_xtiles;
+  dn.C = (uint16_t *)at(o.eout);
+  dn.ldc = H;
+  // the shared expert's gate/up and down run in the same launches as the routed ones
+  if (P.has_shared)
+    shared_gemm_args(L, x, T, (uint16_t *)at(o.shared_act), (uint16_t *)at(o.shared_out), P.sgu, P.sdn);
+  auto paired_x = [&](GemmArgs &g) {
+    GemmArgs t = g;
+    t.xsum = xs_x;
+    t.xsum_ld = H / gu_w.group_size;
+    t.A = (const uint16_t *)at(o.xpair);
+    t.lda = H;
+    t.a_paired = 1;
+    if (gu_w.bits == 4 && t.group == gu_w.group_size && xq_supported(t)) g = t;
+  };
+  auto paired_act = [&](GemmArgs &up, GemmArgs &down, float *sums) {
+    if (!up.a_paired) return false;
+    GemmArgs u = up, d = down;
+    u.c_paired = 1;
+    u.c_xsum = sums;
+    u.c_xsum_ld = down.K / down.group;
+    u.c_group = down.group;
+    d.a_paired = 1;
+    d.xsum = sums;
+    d.xsum_ld = u.c_xsum_ld;
+    if (!xq_supported(u) || !xq_supported(d)) return false;
+    up = u;
+    down = d;
+    return true;
+  };
+  paired_x(gu);
+  if (P.has_shared) paired_x(P.sgu);
+  P.paired_x = gu.a_paired || (P.has_shared && P.sgu.a_paired);
+  P.act_paired = paired_act(gu, dn, xs_act);
+  if (P.has_shared) paired_act(P.sgu, P.sdn, xs_sact);
+  return P;
+}
+
 hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk, const uint32_t *ids,
                       const uint16_t *scores, const Layout &o, char *ws, bool with_shared, uint16_t *y,
                       hipStream_t s, StageClock *clock, bool force_unsorted = false) {
@@ -364,102 +460,36 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
   auto end = [&](int i) {
     if (clock) clock->end(i);
   };
-  const int H = L.hidden, I = L.intermediate, A = T * kk;
+  const int H = L.hidden, A = T * kk;
   const int E = std::max(L.num_experts, expert_capacity(L));
-  uint32_t *sorted_order = (uint32_t *)at(o.sorted_order);
   uint32_t *inverse = (uint32_t *)at(o.inverse);
-  uint32_t *sorted_ids = (uint32_t *)at(o.sorted_ids);
-  uint32_t *offsets = (uint32_t *)at(o.offsets);
-  uint32_t *tile_expert = (uint32_t *)at(o.tile_expert);
-  uint32_t *tile_row0 = (uint32_t *)at(o.tile_row0);
-  uint32_t *tile_count = (uint32_t *)at(o.tile_count);
-  uint16_t *act = (uint16_t *)at(o.act);
   uint16_t *eout = (uint16_t *)at(o.eout);
   uint16_t *sparse = (uint16_t *)at(o.sparse);
-  const bool has_shared = with_shared && L.shared_intermediate > 0;
+  SparsePlan P = plan_sparse(L, x, T, kk, o, ws, with_shared);
+  const bool has_shared = P.has_shared;
+  GemmArgs &gu = P.gu, &dn = P.dn, &sgu = P.sgu, &sdn = P.sdn;
   uint16_t *shared_out = has_shared ? (uint16_t *)at(o.shared_out) : nullptr;
   uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
+  const astro_moe_affine &gu_w = L.gate_up.w ? L.gate_up : L.gate;
 
   begin(2);
-  hipError_t e = launch_sort(ids, A, E, sorted_order, inverse, sorted_ids, offsets, tile_expert, tile_row0,
-                             tile_count, (uint32_t *)at(o.sort_scratch), s);
+  hipError_t e = launch_sort(ids, A, E, (uint32_t *)at(o.sorted_order), inverse, (uint32_t *)at(o.sorted_ids),
+                             (uint32_t *)at(o.offsets), (uint32_t *)at(o.tile_expert), (uint32_t *)at(o.tile_row0),
+                             (uint32_t *)at(o.tile_count), (uint32_t *)at(o.sort_scratch), s,
+                             (uint32_t *)at(o.xtiles));
   end(2);
   if (e != hipSuccess) return e;
-  // 4-bit projections run with exact codes on the group sums of their activation rows
-  const astro_moe_affine &gu_w = L.gate_up.w ? L.gate_up : L.gate;
-  float *xs_x = (float *)at(o.xsum_x), *xs_act = (float *)at(o.xsum_act), *xs_sact = (float *)at(o.xsum_sact);
-  const bool xq_gu = gu_w.bits == 4, xq_dn = L.down.bits == 4;
-  const bool xq_sgu = has_shared && L.shared_gate.bits == 4 && L.shared_gate.group_size == gu_w.group_size;
-  const bool xq_sdn = has_shared && L.shared_down.bits == 4;
-
-  // gate/up with the SwiGLU epilogue: rows gathered as x[sorted_order[r] / kk]
-  GemmArgs gu{};
-  gu.A = x;
-  gu.lda = H;
-  gu.a_rows = sorted_order;
-  gu.a_div = kk;
-  gu.K = H;
-  gu.N = I;
-  if (L.gate_up.w)
-    set_weights(gu, L.gate_up, &L.gate_up, I);
-  else
-    set_weights(gu, L.gate, &L.up, 0);
-  gu.tile_expert = tile_expert;
-  gu.tile_row0 = tile_row0;
-  gu.tile_count = tile_count;
-  gu.expert_offsets = offsets;
-  gu.max_tiles = o.max_tiles;
-  gu.C = act;
-  gu.ldc = I;
-  // the shared expert's gate/up and down run in the same launches as the routed ones
-  GemmArgs sgu, sdn;
-  if (has_shared)
-    shared_gemm_args(L, x, T, (uint16_t *)at(o.shared_act), shared_out, sgu, sdn);
   begin(3);
-  // x's group sums and its copy in the codes' pairing, for the exact-code gate/up
-  uint16_t *xpair = (uint16_t *)at(o.xpair);
-  if (xq_gu || xq_sgu) e = launch_group_sums(x, H, T, H, gu_w.group_size, xs_x, H / gu_w.group_size, xpair, s);
-  auto paired_x = [&](GemmArgs &g) {
-    g.xsum = xs_x;
-    g.xsum_ld = H / gu_w.group_size;
-    g.A = xpair;
-    g.lda = H;
-    g.a_paired = 1;
-  };
-  if (xq_gu) paired_x(gu);
-  if (xq_sgu) paired_x(sgu);
-  // the shared expert's tiles (whole 128-row tiles) first: the dispatcher deals workgroups in
-  // order, so the lighter routed tiles fill the last, partial round of the grid
+  if (P.paired_x)
+    e = launch_group_sums(x, H, T, H, gu_w.group_size, (float *)at(o.xsum_x), H / gu_w.group_size,
+                          (uint16_t *)at(o.xpair), s);
+  // the shared expert's tiles (whole tiles) first: the dispatcher deals workgroups in order, so
+  // the lighter routed tiles fill the last, partial round of the grid
   if (e == hipSuccess)
     e = has_shared ? launch_grouped_gemm2(sgu, &gu, kEpiSwiglu, s) : launch_grouped_gemm2(gu, nullptr, kEpiSwiglu, s);
   end(3);
 
-  GemmArgs dn{};
-  dn.A = act;
-  dn.lda = I;
-  dn.a_div = 1;
-  dn.K = I;
-  dn.N = H;
-  set_weights(dn, L.down, nullptr, 0);
-  dn.tile_expert = tile_expert;
-  dn.tile_row0 = tile_row0;
-  dn.tile_count = tile_count;
-  dn.expert_offsets = offsets;
-  dn.max_tiles = o.max_tiles;
-  dn.C = eout;
-  dn.ldc = H;
   begin(4);
-  if (e == hipSuccess && xq_dn) {
-    e = launch_group_sums(act, I, A, I, L.down.group_size, xs_act, I / L.down.group_size, nullptr, s);
-    dn.xsum = xs_act;
-    dn.xsum_ld = I / L.down.group_size;
-  }
-  if (e == hipSuccess && xq_sdn) {
-    const int Is = L.shared_intermediate, gs = L.shared_down.group_size;
-    e = launch_group_sums((const uint16_t *)at(o.shared_act), Is, T, Is, gs, xs_sact, Is / gs, nullptr, s);
-    sdn.xsum = xs_sact;
-    sdn.xsum_ld = Is / gs;
-  }
   if (e == hipSuccess)
     e = has_shared ? launch_grouped_gemm2(sdn, &dn, kEpiPlain, s) : launch_grouped_gemm2(dn, nullptr, kEpiPlain, s);
   end(4);
@@ -720,6 +750,8 @@ int astro_moe_workspace_layout(const astro_moe_layer *layer, int32_t tokens,
   view->tile_row0 = o.decode ? 0 : o.tile_row0;
   view->tile_count = o.decode ? 0 : o.tile_count;
   view->max_tiles = o.decode ? 0 : (size_t)o.max_tiles;
+  view->activated_paired = !o.decode && view->sorted_path &&
+                           plan_sparse(*layer, nullptr, tokens, layer->top_k, o, nullptr, true).act_paired;
   return ok();
 }
 

@@ -949,7 +949,10 @@ hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s) {
 }
 
 bool gemm_fusable(const GemmArgs &a, const GemmArgs &b) {
-  return a.bkind == b.bkind && xq_supported(a) == xq_supported(b) && use_ws(a) == use_ws(b);
+  // one kernel instantiation serves both problems: the same kernel choice, and for the
+  // exact-code kernel the same group size
+  const bool xq = xq_supported(a);
+  return a.bkind == b.bkind && xq == xq_supported(b) && (!xq || a.group == b.group) && use_ws(a) == use_ws(b);
 }
 
 

@@ -56,8 +56,10 @@ __device__ __forceinline__ void ring_barrier() {
 }
 
 // s_waitcnt vmcnt(n) with expcnt and lgkmcnt at their maxima (no wait on them); n is a
-// compile-time constant at every call, so the switch folds to one instruction.
+// compile-time constant at every call, so the switch folds to one instruction.  The empty asm
+// keeps every memory access issued before the call ahead of the wait (the count relies on it).
 __device__ __forceinline__ void wait_vmcnt_le(int n) {
+  asm volatile("" ::: "memory");
   switch (n) {
 #define ASTRO_WAITVM(N) \
   case N:               \

@@ -7,21 +7,30 @@
 // contribution to an output is
 //   sum_k x (s q + b) = s * sum_k x (128 + q) + (b - 128 s) * sum_k x,
 // the MFMA runs on the exact codes (128 + q is bf16 0x4300 | q: one AND-OR makes two of them)
-// into a per-group fp32 partial P, and at the group's end acc += s P + (b - 128 s) X, with X the
-// group's sum of the activation row (GemmArgs::xsum, from group_sums_kernel).  The cheap unpack
-// pairs the codes of inputs (i, i + 4) of each 8-input word, so the activations take the same
-// pairing: permuted in the A fragment, or already permuted in memory (GemmArgs::a_paired, the
-// copy group_sums_kernel writes of x).
+// into a per-group fp32 partial P, folded at the group's end as acc += s P.  The second term,
+// sum_g c[n][g] X[m][g] with c = b - 128 s and X the groups' sums of the activation row
+// (GemmArgs::xsum), is itself a small product over the groups: fp32 MFMAs (16x16x4) add it four
+// groups at a time.  The cheap unpack pairs the codes of inputs (i, i + 4) of each 8-input word,
+// so the activation rows are stored in the same pairing (GemmArgs::a_paired: the copy of x
+// group_sums_kernel writes, or the activated rows the SwiGLU epilogue writes).
 //
-// A workgroup of 8 waves (one per CU) owns a tile of up to 64 rows of one expert and 512 weight
-// rows (plain: 512 output columns; SwiGLU: 256 activated columns = 256 gate + 256 up rows), K
-// stepped by 128.  Wave w owns weight rows 64 w .. +64 (SwiGLU: the gate rows, then the up
-// rows, of 32 columns) and every row block of the tile, and unpacks its own codes into MFMA
-// operands.  LDS: a 2-stage ring of activation and code tiles filled one step ahead by direct
-// global->LDS loads (16-B pieces: 64-B runs of each weight row's codes), the tile rows' group
-// sums (loaded once), and the weight rows' scales and biases in windows of 8 groups (one 16-B
-// piece per row and window, double-buffered), so small per-group values do not cost a cache
-// line request per row and step.
+// A workgroup of 8 waves (one per CU) owns a tile of up to kXqRows rows of one expert and 512
+// weight rows (plain: 512 output columns; SwiGLU: 256 activated columns = 256 gate + 256 up
+// rows), K stepped by 128.  Wave w owns weight rows 64 w .. +64 (SwiGLU: the gate rows, then
+// the up rows, of 32 columns) and every 16-row block of the tile:
+//   - its codes go from HBM straight into its registers: a step's register set, once unpacked,
+//     takes the codes of the step two ahead (two register sets);
+//     lane (column c, quarter q) of a 16-row block loads the words of its inputs per group,
+//     and the MFMA's input order within the group follows that load (any order works when the
+//     activation fragment uses the same one);
+//   - the activation tile (gathered rows) goes through a 3-stage LDS ring filled by direct
+//     global->LDS loads two steps ahead; one barrier per step;
+//   - the scales and biases of the weight rows come in LDS windows of 8 groups (one 16-B piece
+//     per row and window, double-buffered), the tile rows' group sums once per tile.
+// A routed problem's tiles come from the sort's table (GemmArgs::xtiles): every expert's rows
+// split into ceil(rows / kXqRows) tiles of balanced sizes, so no tile holds a small remainder.
+// The SwiGLU epilogue can store the activated rows in the codes' pairing together with their
+// group sums (GemmArgs::c_paired, c_xsum): the inputs of a following exact-code down projection.
 #include "common.h"
 #include "gemm_dev.h"
 #include "kernels.h"
@@ -34,20 +43,40 @@ namespace astro {
 namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int XQ_W = 8;                          // waves per workgroup
-constexpr int XQ_NT = 64 * XQ_W;                 // weight rows per tile
-constexpr int XQ_KS = 128;                       // K per step
-constexpr int XQ_OA = 0;                         // activations: 64 rows x 256 B
-constexpr int XQ_OC = XQ_OA + 64 * 256;          // codes: 512 rows x 64 B
-constexpr int XQ_SLOT = XQ_OC + XQ_NT * 64;      // 48 KB per ring stage
-constexpr int XQ_OX = 2 * XQ_SLOT;               // group sums: 64 rows x G floats (G <= 64)
-constexpr int XQ_OW = XQ_OX + 64 * 64 * 4;       // scale / bias windows: 2 x (512 x 16 B + 512 x 16 B)
-constexpr int XQ_WIN = 2 * XQ_NT * 16;           // one window: scales, then biases
-constexpr int kXqLds = XQ_OW + 2 * XQ_WIN;       // 144 KB
+constexpr int XQ_NT = 512;                              // weight rows per tile
+constexpr int XQ_NBW = 4;                               // 16-row blocks of weight rows per wave
+constexpr int XQ_RW = 16 * XQ_NBW;                      // weight rows per wave
+constexpr int XQ_W = XQ_NT / XQ_RW;                     // waves per workgroup
+constexpr int XQ_KS = 128;                              // K per step
+constexpr int XQ_MT = kXqRows;                          // rows per tile, at most
+constexpr int XQ_NRMAX = XQ_MT / 16;                    // 16-row blocks per tile, at most
+constexpr int XQ_STAGES = 3;                            // activation ring stages
+constexpr int XQ_AR = 96;                               // activation rows loaded per stage (>= XQ_MT)
+constexpr int XQ_ASTAGE = XQ_AR * 256;                  // one stage: XQ_AR rows x 256 B
+constexpr int XQ_ALOADS = XQ_AR * 16 / (64 * XQ_W);     // 16-B pieces per lane and stage
+static_assert(XQ_ALOADS * 64 * XQ_W == XQ_AR * 16, "whole activation pieces per lane");
+static_assert(XQ_MT <= XQ_AR && XQ_MT % 16 == 0, "tile rows within the loaded rows");
+constexpr int XQ_GMAX = 64;                             // groups per row, at most
+constexpr int XQ_OX = XQ_STAGES * XQ_ASTAGE;            // group sums: XQ_MT rows x (G + 4) floats
+constexpr int XQ_OW = XQ_OX + XQ_MT * (XQ_GMAX + 4) * 4;  // scale / bias windows
+constexpr int XQ_WIN = 2 * XQ_NT * 16;                  // one window: scales, then biases
+constexpr int kXqLds = XQ_OW + 2 * XQ_WIN;
+static_assert(XQ_W * 64 == XQ_NT, "one weight row's window piece per lane");
 
-__device__ __forceinline__ int xq_aswz(int r) { return r & 15; }        // 16-B chunk XOR of a 256-B activation row
-__device__ __forceinline__ int xq_cswz(int t) { return (t >> 2) & 3; }  // 16-B piece XOR of a 64-B code row
+// (128 + q) pairs of an 8-code word: inputs (0, 4), (1, 5), (2, 6), (3, 7), as four dwords.
+// mask (0x000f000f, in an SGPR) and k43 (0x43004300, in a VGPR) are not constants to the
+// compiler, so each dword is one v_and_or_b32 (a VOP3 takes no literal) with the compiler
+// tracking the hazards of its result (inline asm would hide them from it).
+__device__ __forceinline__ u32x4 xq_unpack(uint32_t w, uint32_t mask, uint32_t k43) {
+  u32x4 r;
+  r[0] = (w & mask) | k43;
+  r[1] = ((w >> 4) & mask) | k43;
+  r[2] = ((w >> 8) & mask) | k43;
+  r[3] = ((w >> 12) & mask) | k43;
+  return r;
+}
 
 // inputs (0, 4), (1, 5), (2, 6), (3, 7) of 8 consecutive bf16 values: the codes' pairing
 __device__ __forceinline__ u32x4 xq_pair(const u32x4 &d) {
@@ -59,217 +88,286 @@ __device__ __forceinline__ u32x4 xq_pair(const u32x4 &d) {
   return a;
 }
 
-// EPI: epilogue; GS: 32-input steps per group (1, 2, 4); PAIRED: the activation rows are stored
-// in the codes' pairing.
-template <int EPI, int GS, bool PAIRED>
-__global__ __launch_bounds__(64 * XQ_W) void xq_gemm_kernel(const GemmArgs pa, const GemmArgs pb, int split, int nba,
-                                                            int nbb) {
-  extern __shared__ __attribute__((aligned(16))) char xq_lds[];
-  int bx, by;
-  tile_of_block(bx, by);
-  const bool second = bx >= split;
-  const GemmArgs p = second ? pb : pa;
-  int expert, row0, m_valid;
-  if (!gemm_tile(p, bx, by, second, split, second ? nbb : nba, expert, row0, m_valid)) return;
-  const int nblk = by;
+// place of input e of an 8-input chunk in the codes' pairing (0 4 1 5 2 6 3 7)
+__device__ __forceinline__ int xq_pair_pos(int col) { return (col & ~7) | ((col & 3) << 1) | ((col >> 2) & 1); }
+
+// EPI: epilogue; GS: 32-input MFMA steps per group (1, 2, 4); NR: 16-row blocks computed.
+template <int EPI, int GS, int NR>
+__device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, int expert, int row0, int rows) {
+  constexpr int NG = 4 / GS;        // groups per K step
+  constexpr int NC = XQ_NBW * NG;   // code loads per lane and step (blocks x groups)
+  constexpr int SPW = 8 / NG;       // K steps per window of 8 groups
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, kq = lane >> 4;
   const int nk = p.K / XQ_KS;
-  const int G = p.K / p.group;         // groups per row (a multiple of 8)
-  constexpr int SPW = 2 * GS;          // steps per window of 8 groups (8 g / 128)
+  const int G = p.K / p.group;
+  const int xstride = (G + 4) * 4;  // bytes per row of the group sums (padded: no bank conflicts)
 
-  // weight row of tile row t (SwiGLU: wave t / 64's 32 columns, gate rows then up rows)
+  // weight row of tile row t (SwiGLU: wave t / XQ_RW's XQ_RW / 2 columns, gate rows then up rows)
   auto weight_row = [&](int t, bool &upper) {
     int n;
     if (EPI == kEpiSwiglu) {
-      const int u = t & 63;
-      upper = u >= 32;
-      n = nblk * (XQ_NT / 2) + (t >> 6) * 32 + (u & 31);
+      const int u = t % XQ_RW;
+      upper = u >= XQ_RW / 2;
+      n = nblk * (XQ_NT / 2) + (t / XQ_RW) * (XQ_RW / 2) + u % (XQ_RW / 2);
     } else {
       upper = false;
       n = nblk * XQ_NT + t;
     }
     return n < p.N ? n : p.N - 1;  // rows past N load a valid row; never stored
   };
-  // activation source row of tile row r (rows past m_valid read the tile's first row)
+  // activation source row of tile row r (rows past the tile's read its first row)
   auto source_row = [&](int r) {
-    int src = row0 + (r < m_valid ? r : 0);
+    int src = row0 + (r < rows ? r : 0);
     if (p.a_rows) src = (int)(p.a_rows[src] / (uint32_t)p.a_div);
     if (p.a_rows2) src = (int)p.a_rows2[src];
     return src;
   };
 
-  // ---- this lane's sources of the ring loads: 2 activation pieces, 4 code pieces per step
-  const uint16_t *asrc[2];
+  // ---- sources: this lane's activation pieces, code words and window row
+  const uint16_t *asrc[XQ_ALOADS];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = (2 * wave + i) * 64 + lane, r = q >> 4, pc = q & 15;
-    asrc[i] = p.A + (int64_t)source_row(r) * p.lda + 8 * (pc ^ xq_aswz(r));
+  for (int i = 0; i < XQ_ALOADS; ++i) {
+    const int q = (XQ_ALOADS * wave + i) * 64 + lane, r = q >> 4, pc = q & 15;
+    asrc[i] = p.A + (int64_t)source_row(r) * p.lda + 8 * (pc ^ (r & 15));
   }
-  const uint32_t *csrc[4];
+  const uint32_t *csrc[XQ_NBW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int q = (4 * wave + i) * 64 + lane, t = q >> 2, pc = q & 3;
+  for (int nb = 0; nb < XQ_NBW; ++nb) {
     bool up;
-    const int n = weight_row(t, up);
-    csrc[i] = (up ? p.w1 : p.w0) + (int64_t)expert * p.w_expert_stride + (int64_t)n * p.w_row_stride +
-              4 * (pc ^ xq_cswz(t));
+    const int n = weight_row(XQ_RW * wave + 16 * nb + c16, up);
+    csrc[nb] = (up ? p.w1 : p.w0) + (int64_t)expert * p.w_expert_stride + (int64_t)n * p.w_row_stride + GS * kq;
   }
-  // scale / bias windows: this lane's weight row 64 w + lane
   const uint16_t *ssrc, *bsrc;
   {
     bool up;
-    const int n = weight_row(64 * wave + lane, up);
+    const int n = weight_row(XQ_RW * wave + lane, up);
     const int64_t so = (int64_t)expert * p.sb_expert_stride + (int64_t)n * p.sb_row_stride;
     ssrc = (up ? p.s1 : p.s0) + so;
     bsrc = (up ? p.b1 : p.b0) + so;
   }
 
-  auto issue_step = [&](int k) {
-    const int k0 = k * XQ_KS;
-    char *slot = xq_lds + (k & 1) * XQ_SLOT;
+  uint32_t cw[2][XQ_NBW][4];  // code words: register set, 16-row block, word of the step
+  auto issue_codes = [&](auto set_tag, int k) {
+    constexpr int S = decltype(set_tag)::value;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_global_load_lds((const void *)(asrc[i] + k0), (lds_void *)(slot + XQ_OA + (2 * wave + i) * 1024),
-                                       16, 0, 0);
+    for (int nb = 0; nb < XQ_NBW; ++nb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds((const void *)(csrc[i] + k0 / 8), (lds_void *)(slot + XQ_OC + (4 * wave + i) * 1024),
-                                       16, 0, 0);
+      for (int h = 0; h < NG; ++h) {
+        const uint32_t *src = csrc[nb] + k * 16 + h * 4 * GS;
+        if (GS == 1) {
+          cw[S][nb][h] = *src;
+        } else if (GS == 2) {
+          const u32x2 v = *(const u32x2 *)src;
+          cw[S][nb][2 * h] = v[0];
+          cw[S][nb][2 * h + 1] = v[1];
+        } else {
+          const u32x4 v = *(const u32x4 *)src;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) cw[S][nb][j] = v[j];
+        }
+      }
+  };
+  auto issue_act = [&](int st, int k) {
+    char *stage = lds + st * XQ_ASTAGE;
+#pragma unroll
+    for (int i = 0; i < XQ_ALOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void *)(asrc[i] + k * XQ_KS),
+                                       (lds_void *)(stage + (XQ_ALOADS * wave + i) * 1024), 16, 0, 0);
   };
   auto issue_window = [&](int v) {  // groups 8 v .. 8 v + 7 of every weight row
-    char *win = xq_lds + XQ_OW + (v & 1) * XQ_WIN;
+    char *win = lds + XQ_OW + (v & 1) * XQ_WIN;
     __builtin_amdgcn_global_load_lds((const void *)(ssrc + 8 * v), (lds_void *)(win + wave * 1024), 16, 0, 0);
     __builtin_amdgcn_global_load_lds((const void *)(bsrc + 8 * v), (lds_void *)(win + XQ_NT * 16 + wave * 1024), 16,
                                      0, 0);
   };
-  // the tile rows' group sums, once: row r's G floats at XQ_OX + r * 4 G
+  // the tile rows' group sums, once: row r's G floats at XQ_OX + r * xstride (16-B pieces; the
+  // 4 pad floats of a row are not loaded)
   {
-    const int ppr = G / 4, total = 64 * ppr;  // 16-B pieces per row, in all
-    for (int q0 = 0; q0 < total; q0 += 64 * XQ_W) {
-      const int q = q0 + wave * 64 + lane;
-      if (q < total) {
-        const int r = q / ppr, pc = q - r * ppr;
+    const int ppr = G / 4 + 1, total = XQ_MT * ppr;  // pieces per padded row
+    for (int q0 = wave * 64; q0 < total; q0 += 64 * XQ_W) {
+      const int q = q0 + lane, r = q / ppr, pc = q - r * ppr;
+      if (q < total && pc < G / 4)
         __builtin_amdgcn_global_load_lds((const void *)(p.xsum + (int64_t)source_row(r) * p.xsum_ld + 4 * pc),
-                                         (lds_void *)(xq_lds + XQ_OX + (q0 + wave * 64) * 16), 16, 0, 0);
-      }
+                                         (lds_void *)(lds + XQ_OX + q0 * 16), 16, 0, 0);
     }
   }
+  // every step issues the loads of the step two ahead (activations after the step's barrier,
+  // codes once its own are unpacked), past the last step the last one again (into a stage and
+  // register set nothing reads any more): the same count of loads per step keeps the waits
+  // below exact
   issue_window(0);
-  issue_step(0);
+  issue_act(0, 0);
+  issue_codes(std::integral_constant<int, 0>(), 0);
+  issue_act(1, min(1, nk - 1));
+  issue_codes(std::integral_constant<int, 1>(), min(1, nk - 1));
 
-  const int c16 = lane & 15, kq = lane >> 4;
-  const int nrb = (m_valid + 15) >> 4;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 acc[4][4], part[4][4];
+  f32x4 acc[NR][XQ_NBW];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < NR; ++rb)
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      acc[rb][nb] = zero;
-      part[rb][nb] = zero;
-    }
+    for (int nb = 0; nb < XQ_NBW; ++nb) acc[rb][nb] = zero;
+  // opaque to the compiler (see xq_unpack): the mask in an SGPR, the exponent bits in a VGPR
+  uint32_t mask = 0x000f000fu, k43 = 0x43004300u;
+  asm volatile("" : "+s"(mask));
+  asm volatile("" : "+v"(k43));
 
-  auto consume = [&](auto nr_tag) {
-    constexpr int NR = decltype(nr_tag)::value;  // row blocks computed
-    for (int k = 0; k < nk; ++k) {
-      __builtin_amdgcn_s_waitcnt(0x0f70);  // this wave's loads of step k (and its window)
-      ring_barrier();                      // every wave's; every wave is done with step k - 1
-      if (k + 1 < nk) {
-        if ((k + 1) % SPW == 0) issue_window((k + 1) / SPW);
-        issue_step(k + 1);
+  // tail: the last step after the whole pairs.  The compiler drops the loads of its code words
+  // nothing reads, so fewer loads than XQ_ALOADS + NC may follow its own: it waits for every load.
+  auto step = [&](auto set_tag, int k, bool tail) {
+    constexpr int S = decltype(set_tag)::value;  // register set: k % 2
+    // this wave's loads of step k (issued two steps ago) are in; the next step's may not be
+    if (tail) wait_vmcnt_le(0);
+    else wait_vmcnt_le(XQ_ALOADS + NC);
+    ring_barrier();  // every wave's loads of step k are in; every wave is done with step k - 1
+    if (k % SPW == 0 && (k / SPW + 1) * 8 < G) issue_window(k / SPW + 1);
+    const int ka = min(k + 2, nk - 1);
+    const int st = k % 3;
+    issue_act(st == 0 ? 2 : st - 1, ka);  // stage (k + 2) % 3: step k - 1's
+    const char *stage = lds + st * XQ_ASTAGE;
+    const char *win = lds + XQ_OW + ((k / SPW) & 1) * XQ_WIN;
+#pragma unroll
+    for (int h = 0; h < NG; ++h) {
+      const int gg = k * NG + h;  // the group
+      const int gw = gg & 7;      // its place in the window
+      u32x4 bq[XQ_NBW][GS];
+#pragma unroll
+      for (int nb = 0; nb < XQ_NBW; ++nb)
+#pragma unroll
+        for (int jj = 0; jj < GS; ++jj) bq[nb][jj] = xq_unpack(cw[S][nb][h * GS + jj], mask, k43);
+      if (h == NG - 1) issue_codes(std::integral_constant<int, S>(), ka);  // this set is unpacked
+      float sv[XQ_NBW];
+#pragma unroll
+      for (int nb = 0; nb < XQ_NBW; ++nb)
+        sv[nb] = bf2f(*(const uint16_t *)(win + (XQ_RW * wave + 16 * nb + c16) * 16 + 2 * gw));
+      // per 16-row block, in issue order: the next block's activation fragments, the column
+      // blocks' first MFMAs (independent), their next ones (each XQ_NBW MFMAs after the one it
+      // depends on), then the folds
+      auto frags = [&](int rb, u32x4 *af) {
+        const int r = 16 * rb + c16;
+#pragma unroll
+        for (int jj = 0; jj < GS; ++jj)
+          af[jj] = *(const u32x4 *)(stage + r * 256 + 16 * ((4 * GS * h + GS * kq + jj) ^ (r & 15)));
+      };
+      u32x4 af[2][GS];
+      frags(0, af[0]);
+#pragma unroll
+      for (int rb = 0; rb < NR; ++rb) {
+        if (rb + 1 < NR) frags(rb + 1, af[(rb + 1) & 1]);
+        const u32x4 *a = af[rb & 1];
+        f32x4 pp[XQ_NBW];
+#pragma unroll
+        for (int nb = 0; nb < XQ_NBW; ++nb)
+          pp[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                           __builtin_bit_cast(bf16x8, bq[nb][0]), zero, 0, 0, 0);
+#pragma unroll
+        for (int jj = 1; jj < GS; ++jj)
+#pragma unroll
+          for (int nb = 0; nb < XQ_NBW; ++nb)
+            pp[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[jj]),
+                                                             __builtin_bit_cast(bf16x8, bq[nb][jj]), pp[nb], 0, 0, 0);
+#pragma unroll
+        for (int nb = 0; nb < XQ_NBW; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[rb][nb][i] = __builtin_fmaf(sv[nb], pp[nb][i], acc[rb][nb][i]);
       }
-      const char *slot = xq_lds + (k & 1) * XQ_SLOT;
-      const char *win = xq_lds + XQ_OW + ((k / SPW) & 1) * XQ_WIN;
+      // groups gg - 3 .. gg complete: acc += X[rows][4 groups] . c[4 groups][columns]
+      if (gg % 4 == 3) {
+        const int g4 = gg >> 2;
+        const int gl = (4 * g4 + kq) & 7;  // this lane's group in the window
+        float cq[XQ_NBW];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // B: the wave's four 16-row blocks, inputs 32 j + 8 kq .. +8 as (128 + q) pairs (i, i + 4)
-        u32x4 bq[4];
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          const int t = 64 * wave + 16 * nb + c16;
-          const uint32_t wd = *(const uint32_t *)(slot + XQ_OC + t * 64 + 16 * (j ^ xq_cswz(t)) + 4 * kq);
-          bq[nb][0] = (wd & 0x000f000fu) | 0x43004300u;
-          bq[nb][1] = ((wd >> 4) & 0x000f000fu) | 0x43004300u;
-          bq[nb][2] = ((wd >> 8) & 0x000f000fu) | 0x43004300u;
-          bq[nb][3] = ((wd >> 12) & 0x000f000fu) | 0x43004300u;
+        for (int nb = 0; nb < XQ_NBW; ++nb) {
+          const int t = XQ_RW * wave + 16 * nb + c16;
+          const float s = bf2f(*(const uint16_t *)(win + t * 16 + 2 * gl));
+          const float b = bf2f(*(const uint16_t *)(win + XQ_NT * 16 + t * 16 + 2 * gl));
+          cq[nb] = __builtin_fmaf(-128.0f, s, b);
         }
-        u32x4 af[NR];
 #pragma unroll
         for (int rb = 0; rb < NR; ++rb) {
-          const int r = 16 * rb + c16;
-          const u32x4 d = *(const u32x4 *)(slot + XQ_OA + r * 256 + 16 * ((4 * j + kq) ^ xq_aswz(r)));
-          af[rb] = PAIRED ? d : xq_pair(d);
-        }
-        // the first 32-input step of a group starts its partials afresh
-        constexpr bool fresh_always = GS == 1;
-        const bool fresh = fresh_always || j % GS == 0;
+          const float xa = *(const float *)(lds + XQ_OX + (16 * rb + c16) * xstride + 4 * (4 * g4 + kq));
 #pragma unroll
-        for (int rb = 0; rb < NR; ++rb)
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb)
-            part[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[rb]),
-                                                                   __builtin_bit_cast(bf16x8, bq[nb]),
-                                                                   fresh ? zero : part[rb][nb], 0, 0, 0);
-        // the group ends with this 32-input step: acc += s P + (b - 128 s) X
-        if ((j + 1) % GS == 0) {
-          const int gg = (k * XQ_KS + 32 * (j + 1)) / (32 * GS) - 1;  // the group
-          const int gw = gg & 7;                                     // its place in the window
-          float sv[4], cv[4];
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb) {
-            const int t = 64 * wave + 16 * nb + c16;
-            const float s = bf2f(*(const uint16_t *)(win + t * 16 + 2 * gw));
-            sv[nb] = s;
-            cv[nb] = __builtin_fmaf(-128.0f, s, bf2f(*(const uint16_t *)(win + XQ_NT * 16 + t * 16 + 2 * gw)));
-          }
-#pragma unroll
-          for (int rb = 0; rb < NR; ++rb) {
-            float xs[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              xs[i] = *(const float *)(xq_lds + XQ_OX + (16 * rb + 4 * kq + i) * (4 * G) + 4 * gg);
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                acc[rb][nb][i] = __builtin_fmaf(cv[nb], xs[i], __builtin_fmaf(sv[nb], part[rb][nb][i], acc[rb][nb][i]));
-          }
+          for (int nb = 0; nb < XQ_NBW; ++nb)
+            acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, cq[nb], acc[rb][nb], 0, 0, 0);
         }
       }
     }
   };
-  if (nrb <= 1) consume(std::integral_constant<int, 1>());
-  else if (nrb <= 2) consume(std::integral_constant<int, 2>());
-  else if (nrb <= 3) consume(std::integral_constant<int, 3>());
-  else consume(std::integral_constant<int, 4>());
+  // whole pairs of steps, then the last one: on every path into a step the same loads follow
+  // its codes, so the compiler's own waits for them stay partial
+  int k0 = 0;
+  for (; k0 + 2 <= nk; k0 += 2) {
+    step(std::integral_constant<int, 0>(), k0, false);
+    step(std::integral_constant<int, 1>(), k0 + 1, false);
+  }
+  if (k0 < nk) step(std::integral_constant<int, 0>(), k0, true);
+  wait_vmcnt_le(0);  // the trailing repeated loads, before the ring is reused or the wave ends
 
   // ---- epilogue: lane holds column c16 of each block, rows 4 kq + i
+  if (EPI == kEpiSwiglu) {
+    const bool sums = p.c_xsum != nullptr;
+    float rs[NR][4];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
-    if (rb >= nrb) break;
-    int dsts[4];
+    for (int rb = 0; rb < NR; ++rb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = rb * 16 + kq * 4 + i;
-      const int gr = row0 + (r < m_valid ? r : 0);
-      dsts[i] = p.c_rows ? (int)p.c_rows[gr] : gr;
-    }
+      for (int i = 0; i < 4; ++i) {
+        const int r = rb * 16 + kq * 4 + i;
+        const int gr = row0 + (r < rows ? r : 0);
+        uint16_t *crow = p.C + (int64_t)(p.c_rows ? (int)p.c_rows[gr] : gr) * p.ldc;
+        float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = rb * 16 + kq * 4 + i;
-      if (r >= m_valid) continue;
-      uint16_t *crow = p.C + (int64_t)dsts[i] * p.ldc;
-      if (EPI == kEpiSwiglu) {
-#pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const int col = nblk * (XQ_NT / 2) + wave * 32 + f * 16 + c16;
-          if (col < p.N) crow[col] = (uint16_t)swiglu_bf(round_bf(acc[rb][f][i]), round_bf(acc[rb][f + 2][i]));
+        for (int f = 0; f < XQ_NBW / 2; ++f) {
+          const int col = nblk * (XQ_NT / 2) + wave * (XQ_RW / 2) + f * 16 + c16;
+          const uint32_t a = swiglu_bf(round_bf(acc[rb][f][i]), round_bf(acc[rb][f + XQ_NBW / 2][i]));
+          if (col < p.N) {
+            if (r < rows) crow[p.c_paired ? xq_pair_pos(col) : col] = (uint16_t)a;
+            s += bf2f(a);
+          }
         }
-      } else {
+        rs[rb][i] = s;
+      }
+    if (sums) {
+      // the wave's XQ_RW / 2 columns of each row, then the waves of each group of c_group columns
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          const int col = nblk * XQ_NT + wave * 64 + nb * 16 + c16;
+      for (int rb = 0; rb < NR; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) rs[rb][i] += __shfl_xor(rs[rb][i], o, 16);
+      __syncthreads();  // every wave is done with the ring: its first stage holds the sums
+      float *red = (float *)lds;  // [wave][XQ_MT]
+      if (c16 == 0)
+#pragma unroll
+        for (int rb = 0; rb < NR; ++rb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) red[wave * XQ_MT + rb * 16 + kq * 4 + i] = rs[rb][i];
+      __syncthreads();
+      const int wpg = p.c_group / (XQ_RW / 2);  // waves per group
+      const int gpt = XQ_W / wpg;               // groups of the tile
+      const int g0 = nblk * (XQ_NT / 2) / p.c_group;
+      const int ng = p.N / p.c_group;
+      for (int q = tid; q < rows * gpt; q += 64 * XQ_W) {
+        const int r = q / gpt, j = q - r * gpt;
+        if (g0 + j >= ng) continue;
+        float s = 0.0f;
+        for (int w = 0; w < wpg; ++w) s += red[(j * wpg + w) * XQ_MT + r];
+        const int gr = row0 + r;
+        p.c_xsum[(int64_t)(p.c_rows ? (int)p.c_rows[gr] : gr) * p.c_xsum_ld + g0 + j] = s;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < NR; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = rb * 16 + kq * 4 + i;
+        if (r >= rows) continue;
+        uint16_t *crow = p.C + (int64_t)(p.c_rows ? (int)p.c_rows[row0 + r] : row0 + r) * p.ldc;
+#pragma unroll
+        for (int nb = 0; nb < XQ_NBW; ++nb) {
+          const int col = nblk * XQ_NT + wave * XQ_RW + nb * 16 + c16;
           if (col < p.N) {
             float v = acc[rb][nb][i];
             if (EPI == kEpiBias) v = round_bf(v) + bf2f(p.bias[col]);
@@ -277,8 +375,39 @@ __global__ __launch_bounds__(64 * XQ_W) void xq_gemm_kernel(const GemmArgs pa, c
           }
         }
       }
-    }
   }
+}
+
+template <int EPI, int GS>
+__global__ __launch_bounds__(64 * XQ_W) void xq_gemm_kernel(const GemmArgs pa, const GemmArgs pb, int split, int nba,
+                                                            int nbb) {
+  extern __shared__ __attribute__((aligned(16))) char xq_lds[];
+  int bx, by;
+  tile_of_block(bx, by);
+  const bool second = bx >= split;
+  const GemmArgs p = second ? pb : pa;
+  if (by >= (second ? nbb : nba)) return;
+  const int x = second ? bx - split : bx;
+  int expert = 0, row0, rows;
+  if (p.xtiles) {
+    if (x >= (int)p.xtiles[0]) return;
+    const uint32_t e = p.xtiles[2 + 2 * x];
+    expert = (int)(e & 0xffffu);
+    rows = (int)(e >> 16);
+    row0 = (int)p.xtiles[3 + 2 * x];
+  } else {
+    row0 = x * XQ_MT;
+    rows = min(XQ_MT, p.M - row0);
+  }
+  if (rows <= 0) return;
+  const int nr = (rows + 15) >> 4;
+  if (nr <= 1) xq_tile<EPI, GS, 1>(p, xq_lds, by, expert, row0, rows);
+  else if (nr == 2) xq_tile<EPI, GS, 2>(p, xq_lds, by, expert, row0, rows);
+  else if (nr == 3) xq_tile<EPI, GS, 3>(p, xq_lds, by, expert, row0, rows);
+  else if (XQ_NRMAX == 4 || nr == 4) xq_tile<EPI, GS, 4>(p, xq_lds, by, expert, row0, rows);
+  else if (XQ_NRMAX == 5 || nr == 5) xq_tile<EPI, GS, (XQ_NRMAX < 5 ? 4 : 5)>(p, xq_lds, by, expert, row0, rows);
+  else xq_tile<EPI, GS, XQ_NRMAX>(p, xq_lds, by, expert, row0, rows);
+  static_assert(XQ_NRMAX >= 4 && XQ_NRMAX <= 6, "tiles of 64 to 96 rows");
 }
 
 // X[r][gi] = the fp32 sum of inputs gi * g .. + g of row r (in input order): the group sums of
@@ -303,23 +432,38 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t *__restr
   X[(int64_t)r * ldx + gi] = sum;
 }
 
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 }  // namespace
 
 bool xq_supported(const GemmArgs &a) {
   // 4-bit weights, K steps of 128, groups of 32 / 64 / 128 with a multiple of 8 of them per row
-  // (16-B windows of scales), the activation rows' group sums at hand, 16-B aligned rows
-  if (a.bkind != kBQ4 || !a.xsum || a.K % XQ_KS != 0) return false;
-  if (a.group != 32 && a.group != 64 && a.group != 128) return false;
+  // (16-B windows of scales), the activation rows paired and their group sums at hand, 16-B
+  // aligned rows
+  if (a.bkind != kBQ4 || !a.xsum || !a.a_paired || a.K % XQ_KS != 0) return false;
+  // (groups of 128 need more registers than the tile leaves: the dequantising kernels take them)
+  if (a.group != 32 && a.group != 64) return false;
   const int G = a.K / a.group;
-  return G % 8 == 0 && G <= 64 && a.lda % 8 == 0 && a.w_row_stride % 4 == 0 && a.sb_row_stride % 8 == 0 &&
-         a.sb_expert_stride % 8 == 0 && a.xsum_ld % 4 == 0;
+  if (G % 8 != 0 || G > XQ_GMAX) return false;
+  if (a.lda % 8 || a.w_row_stride % 4 || a.sb_row_stride % 8 || a.sb_expert_stride % 8 || a.xsum_ld % 4 ||
+      a.w_expert_stride % 4)
+    return false;
+  if (!aligned16(a.A) || !aligned16(a.w0) || !aligned16(a.s0) || !aligned16(a.b0) || !aligned16(a.xsum)) return false;
+  if (a.w1 && (!aligned16(a.w1) || !aligned16(a.s1) || !aligned16(a.b1))) return false;
+  // the epilogue's pairing and group sums: whole groups of 32 / 64 / 128 activated columns
+  if (a.c_xsum && (a.c_group % (XQ_RW / 2) || a.c_group > 128 || a.N % a.c_group)) return false;
+  return true;
+}
+
+static int xq_max_tiles(const GemmArgs &a) {
+  return a.xtiles ? a.max_xtiles : (a.M + XQ_MT - 1) / XQ_MT;
 }
 
 hipError_t launch_xq(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_t s) {
   auto shape = [&](const GemmArgs &g, int &mt, int &nb) {
     nb = epi == kEpiSwiglu ? (g.N + XQ_NT / 2 - 1) / (XQ_NT / 2) : (g.N + XQ_NT - 1) / XQ_NT;
-    mt = g.tile_expert ? g.max_tiles : (g.M + BM - 1) / BM;
-    mt = mt > 0 && nb > 0 ? (mt + 7) & ~7 : 0;  // one XCD per row tile (see launch_kind)
+    mt = xq_max_tiles(g);
+    mt = mt > 0 && nb > 0 ? (mt + 7) & ~7 : 0;  // one XCD per row tile (tile_of_block)
   };
   int mta, nba, mtb = 0, nbb = 0;
   shape(a, mta, nba);
@@ -334,20 +478,14 @@ hipError_t launch_xq(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_t 
     hipLaunchKernelGGL(kernel, grid, block, kXqLds, s, a, bb, mta, nba, nbb);
     return hipGetLastError();
   };
-  auto by_group = [&](auto epi_tag, auto paired_tag) {
+  auto by_group = [&](auto epi_tag) {
     constexpr int E = decltype(epi_tag)::value;
-    constexpr bool P = decltype(paired_tag)::value;
-    if (a.group == 32) return launch(xq_gemm_kernel<E, 1, P>);
-    if (a.group == 64) return launch(xq_gemm_kernel<E, 2, P>);
-    return launch(xq_gemm_kernel<E, 4, P>);
+    if (a.group == 32) return launch(xq_gemm_kernel<E, 1>);
+    return launch(xq_gemm_kernel<E, 2>);
   };
-  auto by_epi = [&](auto paired_tag) {
-    if (epi == kEpiSwiglu) return by_group(std::integral_constant<int, kEpiSwiglu>(), paired_tag);
-    if (epi == kEpiBias) return by_group(std::integral_constant<int, kEpiBias>(), paired_tag);
-    return by_group(std::integral_constant<int, kEpiPlain>(), paired_tag);
-  };
-  if (a.a_paired) return by_epi(std::true_type());
-  return by_epi(std::false_type());
+  if (epi == kEpiSwiglu) return by_group(std::integral_constant<int, kEpiSwiglu>());
+  if (epi == kEpiBias) return by_group(std::integral_constant<int, kEpiBias>());
+  return by_group(std::integral_constant<int, kEpiPlain>());
 }
 
 hipError_t launch_group_sums(const uint16_t *A, int64_t lda, int rows, int K, int group, float *X, int64_t ldx,

@@ -9,6 +9,9 @@ namespace astro {
 // Rows of one grouped-GEMM tile; also the row granularity of the tile table the sort
 // kernels emit.
 constexpr int kGemmBM = 64;
+// rows per tile of the exact-code GEMM, at most (the sort's second tile table splits every
+// expert's rows into ceil(rows / kXqRows) tiles of balanced sizes)
+constexpr int kXqRows = 80;
 
 enum BKind { kBQ4 = 0, kBQ8 = 1, kBDense = 2 };
 enum Epilogue { kEpiPlain = 0, kEpiSwiglu = 1, kEpiBias = 2 };
@@ -51,6 +54,17 @@ struct GemmArgs {
   const float *xsum;
   int64_t xsum_ld;
   int a_paired;  // the activation rows hold inputs (0, 4), (1, 5), (2, 6), (3, 7) of every 8
+  // exact-code GEMM: the sort's table of balanced tiles of up to kXqRows rows (launch_sort's
+  // xtiles, with room for max_xtiles entries)
+  const uint32_t *xtiles;
+  int max_xtiles;
+  // exact-code SwiGLU epilogue: store the activated rows in the codes' pairing and the fp32
+  // sums of their groups of c_group columns (c_xsum[row][group], row stride c_xsum_ld): the
+  // a_paired / xsum inputs of an exact-code down projection
+  int c_paired;
+  float *c_xsum;
+  int64_t c_xsum_ld;
+  int c_group;
 };
 
 hipError_t launch_grouped_gemm(const GemmArgs &a, int epilogue, hipStream_t s);
@@ -75,14 +89,17 @@ hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int no
 
 // counting sort of assignment ids by expert (stable), plus the grouped-GEMM tile table
 // (tiles of kGemmBM rows).  offsets has E+2 entries (ids >= E land in a trailing
-// bucket that no tile covers).
+// bucket that no tile covers).  With xtiles set, also the exact-code GEMM's table
+// (2 + 2 * sort_max_xtiles(A, E) words): word 0 the tile count, then per tile
+// (expert | rows << 16, first sorted row), experts ascending.
 // scratch: sort_scratch_bytes(A, E) bytes (per-chunk histograms and local ranks)
 hipError_t launch_sort(const uint32_t *ids, int A, int E, uint32_t *sorted_order,
                        uint32_t *inverse_order, uint32_t *sorted_ids, uint32_t *offsets,
                        uint32_t *tile_expert, uint32_t *tile_row0, uint32_t *tile_count,
-                       uint32_t *scratch, hipStream_t s);
+                       uint32_t *scratch, hipStream_t s, uint32_t *xtiles = nullptr);
 size_t sort_scratch_bytes(int A, int E);
 int sort_max_tiles(int A, int E);
+int sort_max_xtiles(int A, int E);
 
 // out[t] = bf16( x[t] . deq(W row n) ) for a few output rows (wave per (token, row)).
 hipError_t launch_qgemv_rows(const uint16_t *x, int T, int K, const uint32_t *w,

@@ -88,9 +88,9 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
     const uint32_t *__restrict__ local_rank, uint32_t *__restrict__ sorted_order,
     uint32_t *__restrict__ inverse_order, uint32_t *__restrict__ sorted_ids,
     uint32_t *__restrict__ offsets, uint32_t *__restrict__ tile_expert,
-    uint32_t *__restrict__ tile_row0, uint32_t *__restrict__ tile_count) {
+    uint32_t *__restrict__ tile_row0, uint32_t *__restrict__ tile_count, uint32_t *__restrict__ xtiles) {
   __shared__ uint32_t base[kMaxBuckets];
-  __shared__ uint32_t wsum[3][kChunk / 64];
+  __shared__ uint32_t wsum[4][kChunk / 64];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int nb = E + 1;
   const int c = blockIdx.x;
@@ -122,31 +122,37 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
   // first in the table and the smaller last tiles after all of them: the GEMMs deal tiles in
   // table order, so the light tiles fill the grid's last, partial round
   const uint32_t big = e < E ? total / kGemmBM + (total % kGemmBM > kGemmBM / 2 ? 1u : 0u) : 0u;
+  // the exact-code GEMM's tiles: ceil(total / kXqRows) of balanced sizes per expert
+  const uint32_t xt = e < E ? (total + kXqRows - 1) / kXqRows : 0u;
   uint32_t extra_total = 0, extra_pre = 0;
   if (threadIdx.x == 0 && nb > kChunk) sums(kChunk, extra_total, extra_pre);
-  // block inclusive scans of total, tiles and big tiles
-  uint32_t it = total, ip = tiles, ib = big;
+  // block inclusive scans of total, tiles, big tiles and exact-code tiles
+  uint32_t it = total, ip = tiles, ib = big, ix = xt;
   for (int off = 1; off < 64; off <<= 1) {
     const uint32_t o = (uint32_t)__shfl_up((int)it, off, kWave);
     const uint32_t q = (uint32_t)__shfl_up((int)ip, off, kWave);
     const uint32_t g = (uint32_t)__shfl_up((int)ib, off, kWave);
+    const uint32_t h = (uint32_t)__shfl_up((int)ix, off, kWave);
     if (lane >= off) {
       it += o;
       ip += q;
       ib += g;
+      ix += h;
     }
   }
   if (lane == 63) {
     wsum[0][w] = it;
     wsum[1][w] = ip;
     wsum[2][w] = ib;
+    wsum[3][w] = ix;
   }
   __syncthreads();
-  uint32_t bt = 0, bp = 0, bb = 0, big_all = 0;
+  uint32_t bt = 0, bp = 0, bb = 0, bx = 0, big_all = 0;
   for (int v = 0; v < w; ++v) {
     bt += wsum[0][v];
     bp += wsum[1][v];
     bb += wsum[2][v];
+    bx += wsum[3][v];
   }
   for (int v = 0; v < kChunk / 64; ++v) big_all += wsum[2][v];
   const uint32_t off_e = bt + it - total;
@@ -161,9 +167,20 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
         tile_expert[t] = (uint32_t)e;
         tile_row0[t] = off_e + i * kGemmBM;
       }
+      if (xtiles) {
+        // entries (expert | rows << 16, first row) from word 2 on; word 0 holds the count
+        const uint32_t x0 = bx + ix - xt;
+        for (uint32_t i = 0; i < xt; ++i) {
+          const uint32_t r0 = (uint32_t)(((uint64_t)i * total) / xt);
+          const uint32_t r1 = (uint32_t)(((uint64_t)(i + 1) * total) / xt);
+          xtiles[2 + 2 * (x0 + i)] = (uint32_t)e | ((r1 - r0) << 16);
+          xtiles[3 + 2 * (x0 + i)] = off_e + r0;
+        }
+      }
       if (e == nb - 1) {  // the last bucket's thread knows the totals
         offsets[nb] = (uint32_t)A;
         *tile_count = bp + ip;
+        if (xtiles) xtiles[0] = bx + ix;
       }
     }
   }
@@ -177,6 +194,11 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
       offsets[kChunk] = off_x;
       offsets[nb] = (uint32_t)A;
       *tile_count = nt;
+      if (xtiles) {
+        uint32_t nx = 0;  // exact-code tiles of buckets 0 .. 1023
+        for (int v = 0; v < kChunk / 64; ++v) nx += wsum[3][v];
+        xtiles[0] = nx;
+      }
     }
   }
   __syncthreads();
@@ -220,6 +242,8 @@ hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int no
 
 int sort_max_tiles(int A, int E) { return A / kGemmBM + E + 1; }
 
+int sort_max_xtiles(int A, int E) { return A / kXqRows + E + 1; }
+
 size_t sort_scratch_bytes(int A, int E) {
   const size_t nchunks = ((size_t)A + kChunk - 1) / kChunk;
   return ((nchunks * ((size_t)E + 1) * 4 + 255) & ~(size_t)255) + (size_t)A * 4;
@@ -228,7 +252,7 @@ size_t sort_scratch_bytes(int A, int E) {
 hipError_t launch_sort(const uint32_t *ids, int A, int E, uint32_t *sorted_order,
                        uint32_t *inverse_order, uint32_t *sorted_ids, uint32_t *offsets,
                        uint32_t *tile_expert, uint32_t *tile_row0, uint32_t *tile_count,
-                       uint32_t *scratch, hipStream_t s) {
+                       uint32_t *scratch, hipStream_t s, uint32_t *xtiles) {
   if (E < 1 || E + 1 > kMaxBuckets) return hipErrorInvalidValue;
   const int nchunks = (A + kChunk - 1) / kChunk;
   uint32_t *hist = scratch;
@@ -242,7 +266,7 @@ hipError_t launch_sort(const uint32_t *ids, int A, int E, uint32_t *sorted_order
   }
   hipLaunchKernelGGL(sort_place_kernel, dim3(nchunks > 0 ? nchunks : 1), dim3(kChunk), 0, s, ids, A, E, hist,
                      nchunks, local_rank, sorted_order, inverse_order, sorted_ids, offsets, tile_expert,
-                     tile_row0, tile_count);
+                     tile_row0, tile_count, xtiles);
   return hipGetLastError();
 }
 

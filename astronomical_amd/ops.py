@@ -478,7 +478,8 @@ class MoeBlock:
             inverse_order=get(v.inverse_order, A, np.uint32),
             sorted_ids=get(v.sorted_ids, A, np.uint32),
             expert_offsets=get(v.expert_offsets, E_sort + 1, np.uint32),
-            activated_sorted=get(v.activated, A * v.activated_ld, np.uint16).reshape(A, v.activated_ld)[:, :I],
+            activated_sorted=_unpair(get(v.activated, A * v.activated_ld, np.uint16).reshape(A, v.activated_ld)[:, :I],
+                                     bool(v.activated_paired)),
             expert_out_sorted=get(v.expert_out, A * H, np.uint16).reshape(A, H),
             sparse=get(v.sparse, T * H, np.uint16).reshape(T, H))
         if L.shared_intermediate:
@@ -492,6 +493,15 @@ class MoeBlock:
             out["expert_slots"] = get(v.expert_slots, A, np.uint32).reshape(T, k)
             out["missing_slots"] = int(get(v.missing_slots, 1, np.uint32)[0])
         return out
+
+
+def _unpair(rows: np.ndarray, paired: bool) -> np.ndarray:
+    """Activated rows in natural order: a paired row's 8-element chunks hold 0 4 1 5 2 6 3 7."""
+    if not paired:
+        return rows
+    n = rows.shape[1]
+    c = rows.reshape(rows.shape[0], n // 8, 8)
+    return c[:, :, [0, 2, 4, 6, 1, 3, 5, 7]].reshape(rows.shape[0], n)
 
 
 def router_logits(weights: MoeLayerWeights, x: torch.Tensor) -> torch.Tensor:

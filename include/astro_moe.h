@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ASTRO_MOE_ABI_VERSION 5
+#define ASTRO_MOE_ABI_VERSION 6
 
 enum astro_moe_status {
   ASTRO_MOE_OK = 0,
@@ -121,12 +121,15 @@ typedef struct astro_moe_workspace_view {
   size_t missing_slots;      /* u32: routed experts absent from the page (slot_of_expert set) */
   /* Sorted path only (0 on the decode path): the grouped GEMMs' tile table written by the
    * sort -- u32 tile_expert[max_tiles], u32 tile_row0[max_tiles] (first sorted row of the
-   * tile), u32 tile_count (tiles in use).  Tiles hold up to 128 rows of one expert; every
-   * tile of more than 64 rows is listed before the smaller last tiles. */
+   * tile), u32 tile_count (tiles in use).  Tiles hold up to 64 rows of one expert; every
+   * tile of more than 32 rows is listed before the smaller last tiles. */
   size_t tile_expert;
   size_t tile_row0;
   size_t tile_count;
   size_t max_tiles;          /* entries of tile_expert / tile_row0 (a count, not an offset) */
+  /* 1 when the activated rows are stored in the 4-bit codes' pairing: each 8-element chunk
+   * holds elements 0 4 1 5 2 6 3 7 (exact-code GEMMs, with a 256-byte aligned workspace) */
+  size_t activated_paired;
 } astro_moe_workspace_view;
 
 const char *astro_moe_last_error(void);

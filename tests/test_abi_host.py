@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported(L):
         assert hasattr(lib, n), n
     # and the binding declares exactly those
     assert sorted(L.EXPORTS) == names
-    assert lib.astro_moe_abi_version() == 5
+    assert lib.astro_moe_abi_version() == 6
 
 
 def test_invert_assignment_order_host_entry_point(L):
