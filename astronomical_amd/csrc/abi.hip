@@ -472,21 +472,22 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
   uint16_t *z = has_shared ? (uint16_t *)at(o.z) : nullptr;
   const astro_moe_affine &gu_w = L.gate_up.w ? L.gate_up : L.gate;
 
+  // the sort stage also takes x's group sums and paired copy (the exact-code gate/up's
+  // inputs), so the gate/up stage is the one GEMM launch
   begin(2);
   hipError_t e = launch_sort(ids, A, E, (uint32_t *)at(o.sorted_order), inverse, (uint32_t *)at(o.sorted_ids),
                              (uint32_t *)at(o.offsets), (uint32_t *)at(o.tile_expert), (uint32_t *)at(o.tile_row0),
                              (uint32_t *)at(o.tile_count), (uint32_t *)at(o.sort_scratch), s,
                              (uint32_t *)at(o.xtiles));
+  if (e == hipSuccess && P.paired_x)
+    e = launch_group_sums(x, H, T, H, gu_w.group_size, (float *)at(o.xsum_x), H / gu_w.group_size,
+                          (uint16_t *)at(o.xpair), s);
   end(2);
   if (e != hipSuccess) return e;
   begin(3);
-  if (P.paired_x)
-    e = launch_group_sums(x, H, T, H, gu_w.group_size, (float *)at(o.xsum_x), H / gu_w.group_size,
-                          (uint16_t *)at(o.xpair), s);
   // the shared expert's tiles (whole tiles) first: the dispatcher deals workgroups in order, so
   // the lighter routed tiles fill the last, partial round of the grid
-  if (e == hipSuccess)
-    e = has_shared ? launch_grouped_gemm2(sgu, &gu, kEpiSwiglu, s) : launch_grouped_gemm2(gu, nullptr, kEpiSwiglu, s);
+  e = has_shared ? launch_grouped_gemm2(sgu, &gu, kEpiSwiglu, s) : launch_grouped_gemm2(gu, nullptr, kEpiSwiglu, s);
   end(3);
 
   begin(4);

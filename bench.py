@@ -7,13 +7,18 @@ token through a chain of `--layers` distinct seeded layers (40 x 453 MB of exper
 so the step's ~640 MB of selected pages come from HBM, not the 256 MB Infinity Cache);
 each step is one captured HIP graph.  value = layers * steps / timed seconds.
 
-Also reported: prefill of 2048 tokens (config c2) with per-stage times, the roofline of
-the dominant decode kernel (its average duration from start/stop events attached to its
-own dispatches over K x L eager calls; HBM traffic per launch from the rocprofv3 counter
-summary profiles/decode_traffic.json when present), and the CPU oracle (C restatement of
-the reference op graph) timed on a bounded sample on the host cores.
+Also reported: prefill of 2048 tokens (config c2) with per-stage times and the roofline of its
+two GEMM launches (prefill_roofline: FLOPs per launch over the attributed stage time, against
+the dense bf16 MFMA peak), the roofline of the dominant decode kernel (its average duration
+from start/stop events attached to its own dispatches over K x L eager calls; HBM traffic per
+launch from the rocprofv3 counter summaries profiles/decode_traffic.json and
+profiles/prefill_c2_t2048_traffic.json when present), and the CPU oracle (C restatement of the
+reference op graph): decode and a c2 prefill sample on every usable host core and on one,
+medians of 5 runs.
 --copy-check first runs a plain 1 GiB device-to-device copy three times: the reference
 dispatch that scales the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run.
+--prefill-only runs the c2 prefill alone (the workload of the prefill counter profiles);
+--counter-summary DIR... prints a per-kernel table of rocprofv3 --pmc output and exits.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu]
 """
@@ -52,14 +57,23 @@ def parse():
                    help="skip the side measurements of configs c3 and c4")
     p.add_argument("--verification-only", action="store_true",
                    help="only the MTP verification QMV measurement (one JSON line of its own)")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=20.0,
+                   help="budget of the CPU baseline's decode runs (the prefill samples come on top)")
     p.add_argument("--copy-check", action="store_true",
                    help="run a 1 GiB streaming copy first (counter calibration)")
+    p.add_argument("--prefill-only", action="store_true",
+                   help="only the c2 prefill (one JSON line of its own): the workload of the prefill "
+                        "counter profiles")
+    p.add_argument("--counter-summary", nargs="+", metavar="DIR",
+                   help="summarise rocprofv3 --pmc output directories per kernel (markdown) and exit")
     return p.parse_args()
 
 
 def main():
     args = parse()
+    if args.counter_summary:
+        print(counter_summary(args.counter_summary))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the MoE block's multi-GPU "
                           "sharding (expert parallelism over RCCL) is designed, not built; "
@@ -88,6 +102,10 @@ def main():
         log("copy check: 3 x (1 GiB read + 1 GiB write) elementwise kernel")
     cfg = CF.C1
     nL, K, W = args.layers, args.steps, args.warmup
+    if args.prefill_only:
+        blk = ops.MoeBlock(DS.make_layer_device(cfg, layer=0))
+        print(json.dumps(prefill_c2(CF, DS, torch, blk, args.prefill_iters)))
+        return
 
     # ---------------------------------------------------------------- decode chain
     layers = [DS.make_layer_device(cfg, layer=l) for l in range(nL)]
@@ -176,29 +194,8 @@ def main():
             traffic = int(tr["fetch_bytes"] + tr["write_bytes"])
 
     # ---------------------------------------------------------------- prefill 2048 (c2)
-    T = 2048
-    xp = DS.make_tokens_device(CF.C2, T)
-    yp = torch.empty_like(xp)
-    blk0 = blocks[0]
-    wsp = blk0.workspace(T)
-    for _ in range(3):
-        blk0.forward(xp, out=yp, workspace=wsp)
-    torch.cuda.synchronize()
-    pe0, pe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    pe0.record()
-    for _ in range(args.prefill_iters):
-        blk0.forward(xp, out=yp, workspace=wsp)
-    pe1.record()
-    torch.cuda.synchronize()
-    prefill_ms = pe0.elapsed_time(pe1) / args.prefill_iters
-    prefill_flops = cfg.flops_per_token() * T
-    pst = {}
-    for _ in range(5):
-        _, st = blk0.forward_attributed(xp, out=yp, workspace=wsp)
-        for kname, v in st.items():
-            pst.setdefault(kname, []).append(v)
-    prefill_stage_ms = {kname: statistics.median(v) for kname, v in pst.items()}
-    log(f"prefill: {prefill_ms * 1000:.1f} us")
+    pre = prefill_c2(CF, DS, torch, blocks[0], args.prefill_iters)
+    log(f"prefill: {pre['prefill']['ms'] * 1000:.1f} us")
 
     # ---------------------------------------------------------------- side measurements
     extra = None
@@ -212,7 +209,7 @@ def main():
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(layers[0], toks, cfg, args.cpu_seconds)
+        cpu = cpu_baseline(layers[0], toks, cfg, DS.make_tokens_device(CF.C2, 64, step=2), args.cpu_seconds)
 
     result = {
         "metric": "MoE-layer tokens/s (decode B=1, prefill 2048) + % HBM/MFMA roofline, 1xMI355X",
@@ -254,18 +251,96 @@ def main():
         },
         "decode_kernel_us": {k_: round(v * 1000, 2) for k_, v in kernel_ms.items()},
         "decode_kernel_GBps": {k_: round(kernel_bytes[k_] / (v * 1e-3) / 1e9, 1) for k_, v in kernel_ms.items()},
-        "prefill": {
-            "workload": "c2: c1 shapes, 2048 tokens, sorted path",
-            "ms": round(prefill_ms, 4),
-            "tokens_per_s": round(T / (prefill_ms * 1e-3), 1),
-            "achieved_TFLOPs": round(prefill_flops / (prefill_ms * 1e-3) / 1e12, 2),
-            "frac_of_bf16_peak": round(prefill_flops / (prefill_ms * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 4),
-            "stage_us": {k_: round(v * 1000, 2) for k_, v in prefill_stage_ms.items()},
-        },
+        "prefill": pre["prefill"],
+        "prefill_roofline": pre["prefill_roofline"],
         "other_configs": extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))
+
+
+def prefill_c2(CF, DS, torch, blk, iters):
+    """c2: 2048 tokens through one c1 layer (the sorted path).  Whole-block time from events
+    around `iters` forwards; per-stage device times (median of 5) from the attributed entry
+    point, whose gate/up and down stages are one GEMM launch each.  The roofline of those two
+    launches: FLOPs of the routed and shared projections over the launch's duration, against
+    the dense bf16 MFMA peak; HBM traffic per launch from the counter summary
+    profiles/prefill_c2_t2048_traffic.json when present."""
+    cfg, T = CF.C1, 2048
+    xp = DS.make_tokens_device(CF.C2, T)
+    yp = torch.empty_like(xp)
+    wsp = blk.workspace(T)
+    for _ in range(3):
+        blk.forward(xp, out=yp, workspace=wsp)
+    torch.cuda.synchronize()
+    pe0, pe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    pe0.record()
+    for _ in range(iters):
+        blk.forward(xp, out=yp, workspace=wsp)
+    pe1.record()
+    torch.cuda.synchronize()
+    ms = pe0.elapsed_time(pe1) / iters
+    flops = cfg.flops_per_token() * T
+    pst = {}
+    for _ in range(5):
+        _, st = blk.forward_attributed(xp, out=yp, workspace=wsp)
+        for kname, v in st.items():
+            pst.setdefault(kname, []).append(v)
+    stage_ms = {kname: statistics.median(v) for kname, v in pst.items()}
+    H, I, Is, A = cfg.hidden, cfg.intermediate, cfg.shared_intermediate, T * cfg.top_k
+    gemm_flops = {"gate_up": 2 * A * 2 * I * H + 2 * T * 2 * Is * H, "down": 2 * A * H * I + 2 * T * H * Is}
+    names = {"gate_up": "xq_gemm_kernel<SwiGLU> (c2 routed + shared gate/up)",
+             "down": "xq_gemm_kernel<plain> (c2 routed + shared down)"}
+    traffic = {}
+    tpath = os.path.join(ROOT, "profiles", "prefill_c2_t2048_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f)
+
+    def entry(stage):
+        us = stage_ms[stage] * 1000
+        tf = gemm_flops[stage] / (us * 1e-6) / 1e12
+        t = traffic.get(stage)
+        return {"bound": "mfma", "kernel": names[stage], "achieved": round(tf, 2), "peak": BF16_DENSE_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tf / BF16_DENSE_PEAK_TFLOPS, 4),
+                "traffic": int(t["fetch_bytes"] + t["write_bytes"]) if t else None,
+                "flops_per_launch": int(gemm_flops[stage]), "avg_launch_us": round(us, 2)}
+    dom = max(gemm_flops, key=lambda k_: stage_ms[k_])
+    other = "down" if dom == "gate_up" else "gate_up"
+    roof = entry(dom)
+    roof["next"] = entry(other)
+    return {"prefill": {
+        "workload": "c2: c1 shapes, 2048 tokens, sorted path",
+        "ms": round(ms, 4),
+        "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "achieved_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
+        "frac_of_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 4),
+        "stage_us": {k_: round(v * 1000, 2) for k_, v in stage_ms.items()},
+    }, "prefill_roofline": roof}
+
+
+def counter_summary(dirs):
+    """Per-kernel averages of rocprofv3 --pmc output (the *_counter_collection.csv files under
+    each directory), as a markdown table: one row per kernel, one column per counter, values
+    per dispatch.  Kernel names are cut at their argument list."""
+    import csv
+    import glob
+    agg, disp = {}, {}
+    for d in dirs:
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    k = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+                    agg.setdefault(k, {}).setdefault(r["Counter_Name"], 0.0)
+                    agg[k][r["Counter_Name"]] += float(r["Counter_Value"])
+                    disp.setdefault(k, {}).setdefault(r["Counter_Name"], set()).add((path, r["Dispatch_Id"]))
+    counters = sorted({c for k in agg for c in agg[k]})
+    lines = ["| kernel | dispatches | " + " | ".join(counters) + " |", "|---|---|" + "---|" * len(counters)]
+    for k in sorted(agg, key=lambda k_: -sum(agg[k_].values())):
+        n = max(len(v) for v in disp[k].values())
+        row = [f"{agg[k][c] / len(disp[k][c]):.6g}" if c in agg[k] else "" for c in counters]
+        lines.append(f"| {k} | {n} | " + " | ".join(row) + " |")
+    return "\n".join(lines)
 
 
 def other_configs(CF, DS, ops, torch, K, W, layer_c1):
@@ -627,8 +702,12 @@ def page_load(CF, torch, L, n_experts=16, ids=(1, 3, 4, 6, 8, 10, 12, 15), reps=
             "GBps": round(page.bytes_read / sec / 1e9, 2)}
 
 
-def cpu_baseline(layer_dev, toks, cfg, seconds):
-    """The oracle on the host cores, decode B=1 on a bounded sample of the same tokens."""
+def cpu_baseline(layer_dev, toks, cfg, xprefill, seconds):
+    """The oracle (the C restatement of the reference's op graph, OpenMP over output rows) on the
+    host cores: decode B=1 tokens/s on a bounded sample of the bench's own tokens, and a c2
+    prefill sample (64 tokens, the sorted path), each the median of 5 runs, with every core this
+    process may use and with one.  Cores: the process's CPU set, capped by OMP_NUM_THREADS when
+    the environment sets it (the GPU box's share of its host)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     import torch
@@ -637,19 +716,47 @@ def cpu_baseline(layer_dev, toks, cfg, seconds):
     def host(a):
         return u32_to_numpy(a) if a.dtype == torch.int32 else bf16_to_numpy(a)
     Lh = layer_dev.map(host)
-    cores = min(16, os.cpu_count() or 1)
-    oracle.set_threads(cores)
+    avail = len(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    cores = min(avail, cap) if cap > 0 else avail
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     xs = bf16_to_numpy(toks.reshape(-1, cfg.hidden))
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        i = n % xs.shape[0]
-        oracle.moe_block_forward(Lh, xs[i:i + 1])
-        n += 1
-    el = time.perf_counter() - t0
-    return {"value": round(n / el, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"c1 decode B=1, {n} tokens through layer 0 (oracle C restatement, "
-                      f"OpenMP over output rows), {el:.1f} s"}
+    xp = bf16_to_numpy(xprefill)
+    per_run = seconds / 20.0  # 5 decode runs at each thread count take half the budget
+
+    def decode_run():
+        n, t0 = 0, time.perf_counter()
+        while True:
+            i = n % xs.shape[0]
+            oracle.moe_block_forward(Lh, xs[i:i + 1])
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= per_run:
+                return n / el
+
+    def prefill_run(t):
+        t0 = time.perf_counter()
+        oracle.moe_block_forward(Lh, xp[:t])
+        return t / (time.perf_counter() - t0)
+
+    res = {}
+    for name, threads, tp in (("all", cores, 64), ("one", 1, 16)):
+        oracle.set_threads(threads)
+        dec = statistics.median(decode_run() for _ in range(5))
+        pre = statistics.median(prefill_run(tp) for _ in range(5))
+        res[name] = {"threads": threads, "decode_tokens_per_s": round(dec, 2), "prefill_tokens": tp,
+                     "prefill_tokens_per_s": round(pre, 2)}
+    oracle.set_threads(cores)
+    return {"value": res["all"]["decode_tokens_per_s"], "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"c1 decode B=1 through layer 0, median of 5 runs of {per_run:.1f} s each (oracle C "
+                      f"restatement, OpenMP over output rows); prefill: c2 tokens through the sorted path",
+            "nproc": os.cpu_count(), "affinity_cpus": avail, "cpu_model": model,
+            "one_core": res["one"], "all_cores": res["all"]}
 
 
 if __name__ == "__main__":

@@ -170,10 +170,11 @@ int astro_moe_block_forward_no_alloc(const astro_moe_layer *layer, const uint16_
  * PerformanceAttribution operation timers (crates/model-serving/src/performance_attribution.rs:1-80,
  * performance_attribution/catalog.rs:54,89-91) — but measuring device time rather than
  * graph construction.  stage_ms[ASTRO_MOE_STAGES] receives: router projection, route
- * (softmax/top-k), sort (assignment preparation), gate/up + SwiGLU, down (gathered expert
- * execution), shared expert, combine (weighted reduction).  On the sorted path the shared
- * expert's gate/up and down projections run inside the gate/up and down launches (their
- * tiles follow the routed ones), so its stage holds the output gate only.  A stage that is one kernel is
+ * (softmax/top-k), sort (assignment preparation; with 4-bit gate/up also x's group sums and
+ * its copy in the codes' pairing), gate/up + SwiGLU, down (gathered expert execution), shared
+ * expert, combine (weighted reduction).  On the sorted path the shared expert's gate/up and
+ * down projections run inside the gate/up and down launches (their tiles come before the
+ * routed ones), so its stage holds the output gate only.  A stage that is one kernel is
  * timed by events attached to that kernel's dispatch; other stages by event records around
  * their launches.  The decode path (tokens * top_k <= 64) runs three kernels and reports
  * them as router, gate/up (which also runs the shared expert's gate/up, the routing and
