@@ -389,7 +389,8 @@ typedef struct astro_moe_page_interval {
 
 /* Parses the safetensors framing of `path` (8-byte little-endian length, JSON header of at most
  * 64 MiB) with every check of parse_safetensors_header (safetensors_header.rs:171-276), then
- * looks up one tensor.  shape holds up to 8 dimensions; file_offset is file-relative. */
+ * looks up one tensor.  shape receives the first 8 dimensions and rank the tensor's full rank;
+ * file_offset is file-relative. */
 int astro_moe_safetensors_tensor(const char *path, const char *tensor_name, int32_t *dtype,
                                  int32_t *rank, int64_t *shape, uint64_t *file_offset,
                                  uint64_t *byte_count);
