@@ -244,20 +244,15 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
         sv[nb] = bf2f(*(const uint16_t *)(win + (XQ_RW * wave + 16 * nb + c16) * 16 + 2 * gw));
       // per 16-row block, in issue order: the next block's activation fragments, the column
       // blocks' first MFMAs (independent), their next ones (each XQ_NBW MFMAs after the one it
-      // depends on), then the folds
+      // depends on), then the folds of the previous block, whose MFMAs are done by then: the
+      // VALU folds one block while the MFMA unit runs the next
       auto frags = [&](int rb, u32x4 *af) {
         const int r = 16 * rb + c16;
 #pragma unroll
         for (int jj = 0; jj < GS; ++jj)
           af[jj] = *(const u32x4 *)(stage + r * 256 + 16 * ((4 * GS * h + GS * kq + jj) ^ (r & 15)));
       };
-      u32x4 af[2][GS];
-      frags(0, af[0]);
-#pragma unroll
-      for (int rb = 0; rb < NR; ++rb) {
-        if (rb + 1 < NR) frags(rb + 1, af[(rb + 1) & 1]);
-        const u32x4 *a = af[rb & 1];
-        f32x4 pp[XQ_NBW];
+      auto mfmas = [&](const u32x4 *a, f32x4 *pp) {
 #pragma unroll
         for (int nb = 0; nb < XQ_NBW; ++nb)
           pp[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[0]),
@@ -268,11 +263,23 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
           for (int nb = 0; nb < XQ_NBW; ++nb)
             pp[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[jj]),
                                                              __builtin_bit_cast(bf16x8, bq[nb][jj]), pp[nb], 0, 0, 0);
+      };
+      auto fold = [&](int rb, const f32x4 *pp) {
 #pragma unroll
         for (int nb = 0; nb < XQ_NBW; ++nb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[rb][nb][i] = __builtin_fmaf(sv[nb], pp[nb][i], acc[rb][nb][i]);
+      };
+      u32x4 af[2][GS];
+      f32x4 pp[2][XQ_NBW];
+      frags(0, af[0]);
+#pragma unroll
+      for (int rb = 0; rb < NR; ++rb) {
+        if (rb + 1 < NR) frags(rb + 1, af[(rb + 1) & 1]);
+        mfmas(af[rb & 1], pp[rb & 1]);
+        if (rb > 0) fold(rb - 1, pp[(rb - 1) & 1]);
       }
+      fold(NR - 1, pp[(NR - 1) & 1]);
       // groups gg - 3 .. gg complete: acc += X[rows][4 groups] . c[4 groups][columns]
       if (gg % 4 == 3) {
         const int g4 = gg >> 2;

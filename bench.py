@@ -410,8 +410,14 @@ def other_configs(CF, DS, ops, torch, K, W, layer_c1):
         for l in range(nL4):
             b4[l].forward(xp, out=yp, workspace=ws4)
     ms = time_ms(prefill_pass, 3)
+    us4 = ms * 1000 / nL4
+    # at ~32 rows per expert this shape is bound by its weight bytes: every expert page (gate,
+    # up, down codes + scales + biases) is read once per layer, plus the activations
+    wbytes = c4.experts * c4.page_bytes + 512 * c4.hidden * 2 * 2
+    gbs4 = wbytes / (us4 * 1e-6) / 1e9
     out["c4_prefill"] = dict(workload=f"c4: 512 tokens through each of {nL4} 8-bit layers",
-                             **prefill_entry(c4, 512, ms * 1000 / nL4))
+                             **prefill_entry(c4, 512, us4), weight_bytes_per_layer=int(wbytes),
+                             achieved_GBps=round(gbs4, 1), frac_of_hbm_peak=round(gbs4 / HBM_PEAK_GBS, 4))
     del L4, b4, ws4
     torch.cuda.empty_cache()
     log(f"other configs: {json.dumps(out)}")
