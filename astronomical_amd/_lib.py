@@ -107,6 +107,7 @@ EXPORTS = {
                                            C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
                                            C.c_size_t, C.c_void_p], C.c_int),
     "astro_moe_add": ([C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
+    "astro_moe_selftest_bf16_rounding": ([C.c_void_p, C.c_void_p], C.c_int),
     "astro_moe_last_error": ([], C.c_char_p),
     "astro_moe_abi_version": ([], C.c_int),
     "astro_moe_workspace_bytes": ([C.POINTER(Layer), C.c_int32, C.POINTER(C.c_size_t)], C.c_int),

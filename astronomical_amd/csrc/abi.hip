@@ -1222,6 +1222,13 @@ int astro_moe_add(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out
   return e == hipSuccess ? ok() : hip_fail(op, e);
 }
 
+int astro_moe_selftest_bf16_rounding(uint64_t *mismatches, void *stream) {
+  const char *op = "self-test the bf16 rounding";
+  if (!mismatches) return fail(ASTRO_MOE_INVALID_ARGUMENT, op, "the mismatch counter must be non-null");
+  hipError_t e = launch_selftest_bf16((unsigned long long *)mismatches, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_fail(op, e);
+}
+
 // ------------------------------------------------------------------ the decoder step around the block
 
 int astro_moe_add_rms_norm(const uint16_t *hidden, const uint16_t *attention_out, const uint16_t *norm_weight,

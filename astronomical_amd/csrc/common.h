@@ -18,15 +18,23 @@ __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 
 __device__ __forceinline__ float bf_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
 
-// IEEE round-to-nearest-even fp32 -> bf16 on the bit pattern (NaN stays quiet NaN).
-__device__ __forceinline__ uint32_t f2bf(float f) {
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// IEEE round-to-nearest-even fp32 -> bf16 on the bit pattern, NaN kept quiet with its sign and
+// upper payload ((u >> 16) | 0x40): gfx950's v_cvt_pk_bf16_f32 (the compiler's float -> __bf16,
+// with fp32 denormals kept) returns exactly these bits for all 2^32 inputs
+// (astro_moe_selftest_bf16_rounding checks every one against the bit-pattern rounding).
+__device__ __forceinline__ uint32_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+// the same rounding on the bit pattern (the definition the conversion is checked against)
+__device__ __forceinline__ uint32_t f2bf_bits(float f) {
   const uint32_t u = __float_as_uint(f);
   const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
   return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : rounded;
-}
-__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
-__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return f2bf(lo) | (f2bf(hi) << 16);
 }
 
 // exp(x): Cody-Waite reduction x = n ln2 + r (|r| <= ln2/2), degree-7 Taylor polynomial
@@ -63,11 +71,31 @@ __device__ __forceinline__ float det_sigmoid(float v) {
   return 1.0f / (1.0f + det_expf(-v));
 }
 
+// bf16(det_sigmoid(g)) for every g, mostly without det_sigmoid's exp and IEEE division.
+// 1 / (1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal (1 ulp each), the exponent
+// -g log2 e carried with its rounding error (log2 e as a two-float sum, the product's error by
+// fma) and folded back as 2^x (1 + err ln 2): within 2 fp32 ulps of det_sigmoid over every bf16
+// g with |g| <= 16.  An error that small changes the bf16 rounding only when the fp32 value is
+// within a few ulps of a bf16 rounding midpoint (low 16 bits 0x8000): within 16 ulps of one,
+// and for |g| > 16 or NaN, det_sigmoid decides.  Both paths round to the same bf16, so the
+// result is det_sigmoid's for every input (the SwiGLU parity test sweeps all 2^16 bf16 gates).
+__device__ __forceinline__ float sigmoid_bf(float g) {
+#pragma clang fp contract(off)
+  const float l2e_hi = 1.44269502162933349609375f, l2e_lo = 1.925963033500011079e-8f;
+  const float x = -g * l2e_hi;
+  const float xerr = __builtin_fmaf(-g, l2e_hi, -x) + -g * l2e_lo;
+  const float e = __builtin_amdgcn_exp2f(x) * __builtin_fmaf(xerr, 0.693147180559945309f, 1.0f);
+  float s = __builtin_amdgcn_rcpf(1.0f + e);
+  const uint32_t near_mid = (__float_as_uint(s) & 0xffffu) - (0x8000u - 16u);
+  if (!(__builtin_fabsf(g) <= 16.0f) || near_mid <= 32u) s = det_sigmoid(g);
+  return round_bf(s);
+}
+
 // SwiGLU with the reference's three bf16 roundings (mlx_compiled_swiglu.rs:66-86):
 // s = bf16(sigmoid(g)); a = bf16(g*s); out = bf16(a*u).
 __device__ __forceinline__ uint32_t swiglu_bf(float g, float u) {
 #pragma clang fp contract(off)
-  const float s = round_bf(det_sigmoid(g));
+  const float s = sigmoid_bf(g);
   const float a = round_bf(g * s);
   return f2bf(a * u);
 }

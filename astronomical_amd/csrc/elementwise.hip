@@ -362,6 +362,20 @@ __global__ __launch_bounds__(256) void laguna_route_kernel(const uint16_t *__res
   }
 }
 
+// Every fp32 bit pattern: the conversion the kernels round with (f2bf) against the rounding
+// on the bit pattern (f2bf_bits); mismatches counted into *count (zeroed by the first kernel).
+constexpr int kSelfTestPerThread = 1024;
+__global__ void zero_u64_kernel(unsigned long long *p) { *p = 0; }
+__global__ __launch_bounds__(256) void selftest_bf16_kernel(unsigned long long *count) {
+  const uint32_t base = ((uint32_t)blockIdx.x * 256u + threadIdx.x) * (uint32_t)kSelfTestPerThread;
+  unsigned int bad = 0;
+  for (int j = 0; j < kSelfTestPerThread; ++j) {
+    const float f = __uint_as_float(base + (uint32_t)j);
+    bad += f2bf(f) != f2bf_bits(f);
+  }
+  if (bad) atomicAdd(count, (unsigned long long)bad);
+}
+
 }  // namespace
 
 hipError_t launch_add_rms_norm(const uint16_t *h, const uint16_t *a, const uint16_t *w, float eps, int T,
@@ -417,6 +431,14 @@ hipError_t launch_zero_u32(uint32_t *p, int n, hipStream_t s) {
 hipError_t launch_add_bf16(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(add_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, n, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_selftest_bf16(unsigned long long *count, hipStream_t s) {
+  hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(1), 0, s, count);
+  // 2^32 patterns: 2^14 blocks x 256 threads x 1024
+  static_assert(16384ull * 256 * kSelfTestPerThread == (1ull << 32), "one pass over every pattern");
+  hipLaunchKernelGGL(selftest_bf16_kernel, dim3(16384), dim3(256), 0, s, count);
   return hipGetLastError();
 }
 

@@ -127,6 +127,8 @@ hipError_t launch_gather_assignments(const uint32_t *ids, const uint16_t *scores
                                      const uint32_t *positions, int n, uint32_t *out_ids,
                                      uint16_t *out_scores, hipStream_t s);
 hipError_t launch_add_bf16(const uint16_t *a, const uint16_t *b, int64_t n, uint16_t *out, hipStream_t s);
+// *count = the fp32 bit patterns (all 2^32) whose f2bf differs from f2bf_bits
+hipError_t launch_selftest_bf16(unsigned long long *count, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t *p, int n, hipStream_t s);  // a kernel, safe in graph capture
 // decoder step around the block: r = bf16(h + a) (a nullable; r_out nullable), n = RMSNorm(r)
 // with weight w (H <= 8192)

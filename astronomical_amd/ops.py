@@ -613,6 +613,14 @@ def add(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def selftest_bf16_rounding(device: str | torch.device = "cuda") -> int:
+    """Fp32 bit patterns (of all 2^32) on which the library's bf16 rounding differs from
+    round-to-nearest-even on the bit pattern; 0 when they agree everywhere."""
+    count = torch.zeros(1, dtype=torch.int64, device=device)
+    call("astro_moe_selftest_bf16_rounding", _ptr(count), _stream(count.device))
+    return int(count.item())
+
+
 @dataclass
 class Qwen3_5MoESplitPageRoute:
     """split_page_route.rs:11-16."""

@@ -457,6 +457,15 @@ int astro_synth_normal_bf16(uint16_t *out, int64_t n, uint64_t key, double scale
 int astro_synth_activations(uint16_t *out, int32_t tokens, int32_t hidden, uint64_t key,
                             void *stream);
 
+/*
+ * Self-test of the fp32 -> bf16 rounding every kernel uses (no counterpart in the reference):
+ * the kernels round with gfx950's conversion instruction; this runs it on all 2^32 fp32 bit
+ * patterns against IEEE round-to-nearest-even on the bit pattern (NaN kept quiet) and stores
+ * the number of patterns that differ into *mismatches (device memory, one uint64_t; 0 means
+ * the library's bf16 results are those of the bit-pattern rounding).  Asynchronous on stream.
+ */
+int astro_moe_selftest_bf16_rounding(uint64_t *mismatches, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -204,6 +204,34 @@ def test_swiglu_bit_exact(ops, orc):
     assert np.array_equal(_np(ops.apply_compiled_swiglu(_dev_bf16(g), _dev_bf16(u))), orc.swiglu(g, u))
 
 
+def test_swiglu_every_gate_value(ops, orc):
+    """The kernels' sigmoid takes a hardware exp2/reciprocal path away from bf16 rounding
+    midpoints and the exact one near them: every one of the 2^16 bf16 gate values (signed
+    zeros, denormals, infinities, NaNs included) against the oracle, with up = 1 (the output is
+    bf16(g * bf16(sigmoid(g))) itself), with random up values, and with up values that overflow
+    or underflow the product.  NaN outputs compare as NaN (their payload is not specified)."""
+    g = np.arange(1 << 16, dtype=np.uint16)
+    rng = np.random.default_rng(7)
+    ups = [np.full(g.size, 0x3F80, np.uint16),
+           f32_to_bf16((rng.standard_normal(g.size) * 3).astype(np.float32)),
+           f32_to_bf16(np.full(g.size, 3.0e38, np.float32)),
+           f32_to_bf16(np.full(g.size, -1.5e-38, np.float32))]
+    for i, u in enumerate(ups):
+        got = _np(ops.apply_compiled_swiglu(_dev_bf16(g), _dev_bf16(u)))
+        want = orc.swiglu(g, u)
+        nan_want = (want & 0x7FFF) > 0x7F80
+        nan_got = (got & 0x7FFF) > 0x7F80
+        assert np.array_equal(nan_got, nan_want), f"up set {i}: NaN positions differ"
+        bad = np.flatnonzero((got != want) & ~nan_want)
+        assert bad.size == 0, f"up set {i}: {bad.size} gate values differ, first g=0x{g[bad[0]]:04x}"
+
+
+def test_bf16_rounding_selftest(ops):
+    """gfx950's fp32 -> bf16 conversion, which every kernel rounds with, equals round-to-nearest-
+    even on the bit pattern (the oracle's rounding) for all 2^32 fp32 patterns."""
+    assert ops.selftest_bf16_rounding() == 0
+
+
 def test_weighted_sums_bit_exact(ops, orc, kats):
     rng = np.random.default_rng(4)
     T, k, D = 37, 8, 2048
