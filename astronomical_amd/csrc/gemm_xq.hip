@@ -91,11 +91,19 @@ __device__ __forceinline__ u32x4 xq_pair(const u32x4 &d) {
 // place of input e of an 8-input chunk in the codes' pairing (0 4 1 5 2 6 3 7)
 __device__ __forceinline__ int xq_pair_pos(int col) { return (col & ~7) | ((col & 3) << 1) | ((col >> 2) & 1); }
 
-// EPI: epilogue; GS: 32-input MFMA steps per group (1, 2, 4); NR: 16-row blocks computed.
-template <int EPI, int GS, int NR>
-__device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, int expert, int row0, int rows) {
+// EPI: epilogue; GS: 32-input MFMA steps per group (1, 2, 4); NR: 16-row blocks computed;
+// NBW: 16-row blocks of weight rows per wave: XQ_NBW for a whole tile, half of it for a half
+// tile (weight rows half * NT .. + NT of the N-block's XQ_NT; SwiGLU: its activated columns
+// half * NT / 2 .. + NT / 2).
+template <int EPI, int GS, int NR, int NBW>
+__device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, int half, int expert, int row0,
+                                        int rows) {
+  constexpr int RW = 16 * NBW;      // weight rows per wave
+  constexpr int NT = XQ_W * RW;     // weight rows of the tile
+  static_assert(NBW == XQ_NBW || NBW * 2 == XQ_NBW, "whole or half tiles");
+  static_assert(EPI != kEpiSwiglu || NBW % 2 == 0, "a SwiGLU wave pairs its gate and up blocks");
   constexpr int NG = 4 / GS;        // groups per K step
-  constexpr int NC = XQ_NBW * NG;   // code loads per lane and step (blocks x groups)
+  constexpr int NC = NBW * NG;      // code loads per lane and step (blocks x groups)
   constexpr int SPW = 8 / NG;       // K steps per window of 8 groups
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -104,16 +112,16 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
   const int G = p.K / p.group;
   const int xstride = (G + 4) * 4;  // bytes per row of the group sums (padded: no bank conflicts)
 
-  // weight row of tile row t (SwiGLU: wave t / XQ_RW's XQ_RW / 2 columns, gate rows then up rows)
+  // weight row of tile row t (SwiGLU: wave t / RW's RW / 2 columns, gate rows then up rows)
   auto weight_row = [&](int t, bool &upper) {
     int n;
     if (EPI == kEpiSwiglu) {
-      const int u = t % XQ_RW;
-      upper = u >= XQ_RW / 2;
-      n = nblk * (XQ_NT / 2) + (t / XQ_RW) * (XQ_RW / 2) + u % (XQ_RW / 2);
+      const int u = t % RW;
+      upper = u >= RW / 2;
+      n = nblk * (XQ_NT / 2) + half * (NT / 2) + (t / RW) * (RW / 2) + u % (RW / 2);
     } else {
       upper = false;
-      n = nblk * XQ_NT + t;
+      n = nblk * XQ_NT + half * NT + t;
     }
     return n < p.N ? n : p.N - 1;  // rows past N load a valid row; never stored
   };
@@ -132,27 +140,29 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
     const int q = (XQ_ALOADS * wave + i) * 64 + lane, r = q >> 4, pc = q & 15;
     asrc[i] = p.A + (int64_t)source_row(r) * p.lda + 8 * (pc ^ (r & 15));
   }
-  const uint32_t *csrc[XQ_NBW];
+  const uint32_t *csrc[NBW];
 #pragma unroll
-  for (int nb = 0; nb < XQ_NBW; ++nb) {
+  for (int nb = 0; nb < NBW; ++nb) {
     bool up;
-    const int n = weight_row(XQ_RW * wave + 16 * nb + c16, up);
+    const int n = weight_row(RW * wave + 16 * nb + c16, up);
     csrc[nb] = (up ? p.w1 : p.w0) + (int64_t)expert * p.w_expert_stride + (int64_t)n * p.w_row_stride + GS * kq;
   }
   const uint16_t *ssrc, *bsrc;
   {
     bool up;
-    const int n = weight_row(XQ_RW * wave + lane, up);
+    // the window piece of tile row 64 wave + lane (a half tile's lanes past its NT rows load
+    // its last row into window places nothing reads)
+    const int n = weight_row(min(64 * wave + lane, NT - 1), up);
     const int64_t so = (int64_t)expert * p.sb_expert_stride + (int64_t)n * p.sb_row_stride;
     ssrc = (up ? p.s1 : p.s0) + so;
     bsrc = (up ? p.b1 : p.b0) + so;
   }
 
-  uint32_t cw[2][XQ_NBW][4];  // code words: register set, 16-row block, word of the step
+  uint32_t cw[2][NBW][4];  // code words: register set, 16-row block, word of the step
   auto issue_codes = [&](auto set_tag, int k) {
     constexpr int S = decltype(set_tag)::value;
 #pragma unroll
-    for (int nb = 0; nb < XQ_NBW; ++nb)
+    for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
       for (int h = 0; h < NG; ++h) {
         const uint32_t *src = csrc[nb] + k * 16 + h * 4 * GS;
@@ -204,11 +214,11 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
   issue_codes(std::integral_constant<int, 1>(), min(1, nk - 1));
 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 acc[NR][XQ_NBW];
+  f32x4 acc[NR][NBW];
 #pragma unroll
   for (int rb = 0; rb < NR; ++rb)
 #pragma unroll
-    for (int nb = 0; nb < XQ_NBW; ++nb) acc[rb][nb] = zero;
+    for (int nb = 0; nb < NBW; ++nb) acc[rb][nb] = zero;
   // opaque to the compiler (see xq_unpack): the mask in an SGPR, the exponent bits in a VGPR
   uint32_t mask = 0x000f000fu, k43 = 0x43004300u;
   asm volatile("" : "+s"(mask));
@@ -232,18 +242,18 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
     for (int h = 0; h < NG; ++h) {
       const int gg = k * NG + h;  // the group
       const int gw = gg & 7;      // its place in the window
-      u32x4 bq[XQ_NBW][GS];
+      u32x4 bq[NBW][GS];
 #pragma unroll
-      for (int nb = 0; nb < XQ_NBW; ++nb)
+      for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
         for (int jj = 0; jj < GS; ++jj) bq[nb][jj] = xq_unpack(cw[S][nb][h * GS + jj], mask, k43);
       if (h == NG - 1) issue_codes(std::integral_constant<int, S>(), ka);  // this set is unpacked
-      float sv[XQ_NBW];
+      float sv[NBW];
 #pragma unroll
-      for (int nb = 0; nb < XQ_NBW; ++nb)
-        sv[nb] = bf2f(*(const uint16_t *)(win + (XQ_RW * wave + 16 * nb + c16) * 16 + 2 * gw));
+      for (int nb = 0; nb < NBW; ++nb)
+        sv[nb] = bf2f(*(const uint16_t *)(win + (RW * wave + 16 * nb + c16) * 16 + 2 * gw));
       // per 16-row block, in issue order: the next block's activation fragments, the column
-      // blocks' first MFMAs (independent), their next ones (each XQ_NBW MFMAs after the one it
+      // blocks' first MFMAs (independent), their next ones (each NBW MFMAs after the one it
       // depends on), then the folds of the previous block, whose MFMAs are done by then: the
       // VALU folds one block while the MFMA unit runs the next
       auto frags = [&](int rb, u32x4 *af) {
@@ -254,24 +264,24 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
       };
       auto mfmas = [&](const u32x4 *a, f32x4 *pp) {
 #pragma unroll
-        for (int nb = 0; nb < XQ_NBW; ++nb)
+        for (int nb = 0; nb < NBW; ++nb)
           pp[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[0]),
                                                            __builtin_bit_cast(bf16x8, bq[nb][0]), zero, 0, 0, 0);
 #pragma unroll
         for (int jj = 1; jj < GS; ++jj)
 #pragma unroll
-          for (int nb = 0; nb < XQ_NBW; ++nb)
+          for (int nb = 0; nb < NBW; ++nb)
             pp[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[jj]),
                                                              __builtin_bit_cast(bf16x8, bq[nb][jj]), pp[nb], 0, 0, 0);
       };
       auto fold = [&](int rb, const f32x4 *pp) {
 #pragma unroll
-        for (int nb = 0; nb < XQ_NBW; ++nb)
+        for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[rb][nb][i] = __builtin_fmaf(sv[nb], pp[nb][i], acc[rb][nb][i]);
       };
       u32x4 af[2][GS];
-      f32x4 pp[2][XQ_NBW];
+      f32x4 pp[2][NBW];
       frags(0, af[0]);
 #pragma unroll
       for (int rb = 0; rb < NR; ++rb) {
@@ -284,10 +294,10 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
       if (gg % 4 == 3) {
         const int g4 = gg >> 2;
         const int gl = (4 * g4 + kq) & 7;  // this lane's group in the window
-        float cq[XQ_NBW];
+        float cq[NBW];
 #pragma unroll
-        for (int nb = 0; nb < XQ_NBW; ++nb) {
-          const int t = XQ_RW * wave + 16 * nb + c16;
+        for (int nb = 0; nb < NBW; ++nb) {
+          const int t = RW * wave + 16 * nb + c16;
           const float s = bf2f(*(const uint16_t *)(win + t * 16 + 2 * gl));
           const float b = bf2f(*(const uint16_t *)(win + XQ_NT * 16 + t * 16 + 2 * gl));
           cq[nb] = __builtin_fmaf(-128.0f, s, b);
@@ -296,7 +306,7 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
         for (int rb = 0; rb < NR; ++rb) {
           const float xa = *(const float *)(lds + XQ_OX + (16 * rb + c16) * xstride + 4 * (4 * g4 + kq));
 #pragma unroll
-          for (int nb = 0; nb < XQ_NBW; ++nb)
+          for (int nb = 0; nb < NBW; ++nb)
             acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, cq[nb], acc[rb][nb], 0, 0, 0);
         }
       }
@@ -325,9 +335,9 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
         uint16_t *crow = p.C + (int64_t)(p.c_rows ? (int)p.c_rows[gr] : gr) * p.ldc;
         float s = 0.0f;
 #pragma unroll
-        for (int f = 0; f < XQ_NBW / 2; ++f) {
-          const int col = nblk * (XQ_NT / 2) + wave * (XQ_RW / 2) + f * 16 + c16;
-          const uint32_t a = swiglu_bf(round_bf(acc[rb][f][i]), round_bf(acc[rb][f + XQ_NBW / 2][i]));
+        for (int f = 0; f < NBW / 2; ++f) {
+          const int col = nblk * (XQ_NT / 2) + half * (NT / 2) + wave * (RW / 2) + f * 16 + c16;
+          const uint32_t a = swiglu_bf(round_bf(acc[rb][f][i]), round_bf(acc[rb][f + NBW / 2][i]));
           if (col < p.N) {
             if (r < rows) crow[p.c_paired ? xq_pair_pos(col) : col] = (uint16_t)a;
             s += bf2f(a);
@@ -336,7 +346,7 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
         rs[rb][i] = s;
       }
     if (sums) {
-      // the wave's XQ_RW / 2 columns of each row, then the waves of each group of c_group columns
+      // the wave's RW / 2 columns of each row, then the waves of each group of c_group columns
 #pragma unroll
       for (int rb = 0; rb < NR; ++rb)
 #pragma unroll
@@ -351,9 +361,9 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
 #pragma unroll
           for (int i = 0; i < 4; ++i) red[wave * XQ_MT + rb * 16 + kq * 4 + i] = rs[rb][i];
       __syncthreads();
-      const int wpg = p.c_group / (XQ_RW / 2);  // waves per group
+      const int wpg = p.c_group / (RW / 2);  // waves per group
       const int gpt = XQ_W / wpg;               // groups of the tile
-      const int g0 = nblk * (XQ_NT / 2) / p.c_group;
+      const int g0 = (nblk * (XQ_NT / 2) + half * (NT / 2)) / p.c_group;
       const int ng = p.N / p.c_group;
       for (int q = tid; q < rows * gpt; q += 64 * XQ_W) {
         const int r = q / gpt, j = q - r * gpt;
@@ -373,8 +383,8 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
         if (r >= rows) continue;
         uint16_t *crow = p.C + (int64_t)(p.c_rows ? (int)p.c_rows[row0 + r] : row0 + r) * p.ldc;
 #pragma unroll
-        for (int nb = 0; nb < XQ_NBW; ++nb) {
-          const int col = nblk * XQ_NT + wave * XQ_RW + nb * 16 + c16;
+        for (int nb = 0; nb < NBW; ++nb) {
+          const int col = nblk * XQ_NT + half * NT + wave * RW + nb * 16 + c16;
           if (col < p.N) {
             float v = acc[rb][nb][i];
             if (EPI == kEpiBias) v = round_bf(v) + bf2f(p.bias[col]);
@@ -385,36 +395,102 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
   }
 }
 
-template <int EPI, int GS>
+// Workgroup -> tile.  The 8 XCDs take workgroups round-robin by index, and the dispatcher deals
+// them strictly in order (a workgroup whose XCD has no free CU holds back the ones after it).
+// The tiles are laid out per XCD: XCD j holds the row tiles x = j (mod 8) of both problems, each
+// padded to a multiple of 8, the N-blocks of one row tile one after the other so they share its
+// activation rows in that XCD's L2; the XCD's s-th workgroup takes place s (cx = 0: padded places
+// return at once).
+// With cx > 0 (the XCD's CUs) the real tiles past the XCD's last whole round of cx workgroups
+// form a partial round; when it is at most half full, each of its tiles splits into two half
+// tiles, the second half taken by the workgroups right after the XCD's real tiles (the grid has
+// 8 cx extra workgroups for them), so the partial round takes about as long as a half tile.
+// Then problem a's padding is skipped (its row count is known to the host: a has no tile
+// table, or there is no b), b's real row tiles come first in its places, and both problems
+// have nb N-blocks.  A workgroup's tile does not depend on the device-side tile count except for
+// the second halves: its tile-table entry is loaded together with the count.  SPLIT: the kernel
+// that splits (cx > 0); the other holds no half-tile code.
+template <int EPI, int GS, bool SPLIT>
 __global__ __launch_bounds__(64 * XQ_W) void xq_gemm_kernel(const GemmArgs pa, const GemmArgs pb, int split, int nba,
-                                                            int nbb) {
+                                                            int nbb, int g0, int cx) {
+  if (!SPLIT) cx = 0;
   extern __shared__ __attribute__((aligned(16))) char xq_lds[];
-  int bx, by;
-  tile_of_block(bx, by);
+  const int nb = max(nba, nbb);
+  const int l = (int)blockIdx.x;
+  const int j = l & 7;                                   // the XCD
+  const int S = g0 >> 3;                                 // the XCD's places in the padded layout
+  const int pos = l < g0 ? l >> 3 : S + ((l - g0) >> 3);  // the workgroup's place in the XCD's sequence
+  const int mt = g0 / nb;                                // padded row tiles of both problems
+  const bool has_b = mt > split;
+  const int qa = split >> 3;                             // a's padded row tiles per XCD
+  // a's real row tiles on this XCD when a's padding is skipped (host-known row count)
+  const int na = cx > 0 && has_b ? max(0, min(qa, ((pa.M + XQ_MT - 1) / XQ_MT - j + 7) >> 3)) : qa;
+  // place t of the XCD's sequence (a's padding skipped) -> row tile bx, N-block by
+  auto place = [&](int t, int &bx, int &by) {
+    const int r = t / nb;
+    by = t - r * nb;
+    bx = 8 * (r < na ? r : qa + (r - na)) + j;
+  };
+  // a row tile's table entry (clamped into the table: a place past the real tiles loads a valid
+  // entry that the count check then discards)
+  // (fields picked by value: a reference to a kernel argument would copy both to scratch)
+  auto entry = [&](int bx, uint32_t &e, uint32_t &r0) {
+    const bool second = bx >= split;
+    const uint32_t *xt = second ? pb.xtiles : pa.xtiles;
+    if (xt) {
+      const int x = min(second ? bx - split : bx, (second ? pb.max_xtiles : pa.max_xtiles) - 1);
+      e = xt[2 + 2 * x];
+      r0 = xt[3 + 2 * x];
+    }
+  };
+  int bx, by, half = -1;  // half: -1 whole, 0 / 1 the halves of a split tile
+  place(pos, bx, by);
+  uint32_t e = 0, r0 = 0;
+  entry(bx, e, r0);
+  const int cnt_a = pa.xtiles ? (int)pa.xtiles[0] : (pa.M + XQ_MT - 1) / XQ_MT;
+  const int cnt_b = has_b ? (pb.xtiles ? (int)pb.xtiles[0] : (pb.M + XQ_MT - 1) / XQ_MT) : 0;
+  if (cx > 0) {
+    // the XCD's real tiles
+    const int f = nb * (max(0, min(qa, (cnt_a - j + 7) >> 3)) + max(0, min((mt - split) >> 3, (cnt_b - j + 7) >> 3)));
+    int tail0 = f / cx * cx, tail = f - tail0;
+    if (2 * tail > cx) tail0 = f, tail = 0;  // more than half a round: splitting would not shorten it
+    if (pos >= f) {
+      if (pos - f >= tail) return;
+      place(tail0 + (pos - f), bx, by);
+      entry(bx, e, r0);
+      half = 1;
+    } else if (pos >= tail0) {
+      half = 0;
+    }
+  }
   const bool second = bx >= split;
   const GemmArgs p = second ? pb : pa;
   if (by >= (second ? nbb : nba)) return;
   const int x = second ? bx - split : bx;
+  if (x >= (second ? cnt_b : cnt_a)) return;
   int expert = 0, row0, rows;
   if (p.xtiles) {
-    if (x >= (int)p.xtiles[0]) return;
-    const uint32_t e = p.xtiles[2 + 2 * x];
     expert = (int)(e & 0xffffu);
     rows = (int)(e >> 16);
-    row0 = (int)p.xtiles[3 + 2 * x];
+    row0 = (int)r0;
   } else {
     row0 = x * XQ_MT;
     rows = min(XQ_MT, p.M - row0);
   }
   if (rows <= 0) return;
   const int nr = (rows + 15) >> 4;
-  if (nr <= 1) xq_tile<EPI, GS, 1>(p, xq_lds, by, expert, row0, rows);
-  else if (nr == 2) xq_tile<EPI, GS, 2>(p, xq_lds, by, expert, row0, rows);
-  else if (nr == 3) xq_tile<EPI, GS, 3>(p, xq_lds, by, expert, row0, rows);
-  else if (XQ_NRMAX == 4 || nr == 4) xq_tile<EPI, GS, 4>(p, xq_lds, by, expert, row0, rows);
-  else if (XQ_NRMAX == 5 || nr == 5) xq_tile<EPI, GS, (XQ_NRMAX < 5 ? 4 : 5)>(p, xq_lds, by, expert, row0, rows);
-  else xq_tile<EPI, GS, XQ_NRMAX>(p, xq_lds, by, expert, row0, rows);
+  auto dispatch = [&](auto nbw_tag, int h) {
+    constexpr int W = decltype(nbw_tag)::value;
+    if (nr <= 1) xq_tile<EPI, GS, 1, W>(p, xq_lds, by, h, expert, row0, rows);
+    else if (nr == 2) xq_tile<EPI, GS, 2, W>(p, xq_lds, by, h, expert, row0, rows);
+    else if (nr == 3) xq_tile<EPI, GS, 3, W>(p, xq_lds, by, h, expert, row0, rows);
+    else if (XQ_NRMAX == 4 || nr == 4) xq_tile<EPI, GS, 4, W>(p, xq_lds, by, h, expert, row0, rows);
+    else if (XQ_NRMAX == 5 || nr == 5) xq_tile<EPI, GS, (XQ_NRMAX < 5 ? 4 : 5), W>(p, xq_lds, by, h, expert, row0, rows);
+    else xq_tile<EPI, GS, XQ_NRMAX, W>(p, xq_lds, by, h, expert, row0, rows);
+  };
   static_assert(XQ_NRMAX >= 4 && XQ_NRMAX <= 6, "tiles of 64 to 96 rows");
+  if (!SPLIT || half < 0) dispatch(std::integral_constant<int, XQ_NBW>(), 0);
+  else dispatch(std::integral_constant<int, XQ_NBW / 2>(), half);
 }
 
 // X[r][gi] = the fp32 sum of inputs gi * g .. + g of row r (in input order): the group sums of
@@ -466,29 +542,51 @@ static int xq_max_tiles(const GemmArgs &a) {
   return a.xtiles ? a.max_xtiles : (a.M + XQ_MT - 1) / XQ_MT;
 }
 
+// CUs per XCD of the current device (its 8 XCDs take workgroups round-robin); 0 if unknown
+static int xq_cus_per_xcd() {
+  static int cached[64];  // per device; written once with the same value by any thread
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) return 0;
+    cached[dev] = n / 8;
+  }
+  return cached[dev];
+}
+
 hipError_t launch_xq(const GemmArgs &a, const GemmArgs *b, int epi, hipStream_t s) {
   auto shape = [&](const GemmArgs &g, int &mt, int &nb) {
     nb = epi == kEpiSwiglu ? (g.N + XQ_NT / 2 - 1) / (XQ_NT / 2) : (g.N + XQ_NT - 1) / XQ_NT;
     mt = xq_max_tiles(g);
-    mt = mt > 0 && nb > 0 ? (mt + 7) & ~7 : 0;  // one XCD per row tile (tile_of_block)
+    mt = mt > 0 && nb > 0 ? (mt + 7) & ~7 : 0;  // one XCD per row tile
   };
   int mta, nba, mtb = 0, nbb = 0;
   shape(a, mta, nba);
   if (b) shape(*b, mtb, nbb);
   if (mta + mtb == 0) return hipSuccess;
   const GemmArgs &bb = b ? *b : a;
-  dim3 grid(mta + mtb, std::max(nba, nbb)), block(64 * XQ_W);
+  const int nb = std::max(nba, nbb), g0 = (mta + mtb) * nb;
+  // half tiles of a partial last round: K long enough that a tile's time is mostly its K steps
+  // (a half tile of a few steps takes nearly as long as a whole one), both problems with the
+  // same N-blocks, problem a's row count known here when there is a b (no tile table), and a
+  // half tile's activated columns (XQ_NT / 4) whole groups of the epilogue's sums
+  int cx = a.K / XQ_KS >= 8 ? xq_cus_per_xcd() : 0;
+  if ((mtb > 0 && (nba != nbb || a.xtiles)) || (epi == kEpiSwiglu && a.c_xsum && (XQ_NT / 4) % a.c_group) ||
+      (epi == kEpiSwiglu && mtb > 0 && bb.c_xsum && (XQ_NT / 4) % bb.c_group))
+    cx = 0;
+  dim3 grid(g0 + 8 * cx), block(64 * XQ_W);
   auto launch = [&](auto kernel) {
     // > 64 KB of LDS is an opt-in per kernel (idempotent; cheap next to the launch)
     const hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kXqLds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kernel, grid, block, kXqLds, s, a, bb, mta, nba, nbb);
+    hipLaunchKernelGGL(kernel, grid, block, kXqLds, s, a, bb, mta, nba, nbb, g0, cx);
     return hipGetLastError();
   };
   auto by_group = [&](auto epi_tag) {
     constexpr int E = decltype(epi_tag)::value;
-    if (a.group == 32) return launch(xq_gemm_kernel<E, 1>);
-    return launch(xq_gemm_kernel<E, 2>);
+    if (cx > 0) return a.group == 32 ? launch(xq_gemm_kernel<E, 1, true>) : launch(xq_gemm_kernel<E, 2, true>);
+    return a.group == 32 ? launch(xq_gemm_kernel<E, 1, false>) : launch(xq_gemm_kernel<E, 2, false>);
   };
   if (epi == kEpiSwiglu) return by_group(std::integral_constant<int, kEpiSwiglu>());
   if (epi == kEpiBias) return by_group(std::integral_constant<int, kEpiBias>());
