@@ -160,7 +160,7 @@ Layout block_layout(const astro_moe_layer &L, int T, int kk, bool with_router) {
   o.offsets = take((E + 2) * 4);
   if (o.decode) {
     // n_groups, then expert / first row / count of up to 64 groups
-    o.groups = take(4 + 3 * 64 * 4);
+    o.groups = take(4 + 3 * 64 * 4 + 64 * kDecodeMaxK * 4);  // count, expert / start / rows, tokens
     o.act_ld = std::max<int64_t>(L.intermediate, (int64_t)Is);
     o.act = take((A + (Is ? T : 0)) * (size_t)o.act_ld * 2);
     o.eout = take((A + (Is ? T : 0)) * (size_t)L.hidden * 2);
@@ -649,6 +649,7 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
     d.g_expert = groups + 1;
     d.g_start = groups + 1 + 64;
     d.g_count = groups + 1 + 128;
+    d.g_tokens = groups + 1 + 192;
     d.act = act;
     d.act_ld = o.act_ld;
     d.down_out = eout;

@@ -211,23 +211,25 @@ __device__ __forceinline__ void rows_task(const uint32_t *gw, const uint16_t *gs
   }
 }
 
-// rows_task over at most 4 tokens at a time: more tokens run as passes of 4 over the same
-// rows (the second reads the codes from L2), which keeps the kernel's registers at the
-// 4-token footprint; each token's sums are the same either way.
+// rows_task over a few tokens at a time: more tokens run as passes over the same rows (the
+// later ones read the codes from L2), which keeps the kernel's registers at the footprint of
+// one pass -- kDecodePassTokens tokens for waves of several row pairs, 4 for one row pair --
+// and so more waves per SIMD; each token's sums are the same either way.
 template <int BITS, int MT, int RP, bool SWIGLU, int NC>
 __device__ __forceinline__ void rows_task_q(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb,
                                             const uint32_t *uw, const uint16_t *us, const uint16_t *ub,
                                             int64_t w_rs, int64_t sb_rs, int nrows, int nchunks, int group,
                                             const uint16_t *x, int64_t ldx, const int *xrows, int m, uint16_t *out,
                                             int64_t ldo, const int *orows) {
-  if constexpr (MT <= 4) {
+  constexpr int PT = RP > 1 ? kDecodePassTokens : 4;  // tokens per pass
+  if constexpr (MT <= PT) {
     rows_task<BITS, MT, RP, SWIGLU, NC>(gw, gs, gb, uw, us, ub, w_rs, sb_rs, nrows, nchunks, group, x, ldx, xrows,
                                         m, out, ldo, orows);
   } else {
-    for (int t0 = 0; t0 < MT; t0 += 4) {
+    for (int t0 = 0; t0 < MT; t0 += PT) {
       if (t0 >= m) break;
-      rows_task<BITS, 4, RP, SWIGLU, NC>(gw, gs, gb, uw, us, ub, w_rs, sb_rs, nrows, nchunks, group, x, ldx,
-                                         xrows + t0, m - t0 < 4 ? m - t0 : 4, out, ldo, orows + t0);
+      rows_task<BITS, PT, RP, SWIGLU, NC>(gw, gs, gb, uw, us, ub, w_rs, sb_rs, nrows, nchunks, group, x, ldx,
+                                          xrows + t0, m - t0 < PT ? m - t0 : PT, out, ldo, orows + t0);
     }
   }
 }
@@ -348,15 +350,19 @@ __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) 
 
 // ---------------------------------------------------------------- D2: route + gate/up
 
+// what decode_route writes to the workspace: the routing (ids, scores, sort, inverse, sorted
+// ids, offsets) and the distinct-expert table (count, expert / first row / rows, tokens)
+constexpr int kPublishRoute = 1, kPublishTable = 2;
+
 // Routing of the <= 8 tokens from their logits, the stable sort of the <= 64 assignments and
-// the table of distinct experts, into LDS; with publish, also written to the workspace for the
-// later kernels (ids, scores, sort, inverse, offsets, the table).  EXACT: each token's slice in
-// the order of MLX's CPU argpartition (route_token_exact; waves 0 .. route_waves - 1 route, each
-// with kSelectWords<PER> words of sel_sh); otherwise the slice in ascending key order (route_token), which
-// gives the same set, hence the same distinct-expert table and rows per expert, but not the same
-// slot order -- enough for the gate/up GEMVs, not for anything published.
+// the table of distinct experts, into LDS; publish (kPublish* bits) selects what is also written
+// to the workspace for the later kernels.  EXACT: each token's slice in the order of MLX's CPU
+// argpartition (route_token_exact; waves 0 .. route_waves - 1 route, each with
+// kSelectWords<PER> words of sel_sh); otherwise the slice in ascending key order (route_token),
+// which gives the same set, hence the same distinct-expert table and rows per expert, but not
+// the same slot order -- enough for the table, not for the routing.
 template <int MT, int PER, bool EXACT>
-__device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, uint32_t *idx_sh, uint32_t *so_sh,
+__device__ __forceinline__ void decode_route(const DecodeArgs &p, int publish, uint32_t *idx_sh, uint32_t *so_sh,
                                              uint32_t *sid_sh, uint32_t *key_sh, uint32_t (*route_sh)[kDecodeMaxK],
                                              uint16_t *sc_sh, uint32_t *g_expert_sh, uint32_t *g_start_sh,
                                              uint32_t *g_count_sh, uint32_t &ng_sh, uint32_t *sel_sh = nullptr,
@@ -410,7 +416,7 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, 
       g_count_sh[gi] = (uint32_t)(next - lane);
     }
     if (lane == 0) ng_sh = (uint32_t)__popcll(mask);
-    if (publish) {
+    if (publish & kPublishRoute) {
       if (lane < A) {
         p.idx[lane] = idx_sh[lane];
         p.scores[lane] = sc_sh[lane];
@@ -418,16 +424,32 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, 
         p.inverse_order[lane] = rank;
         p.sorted_ids[rank] = key >> 6;
       }
+    }
+    if (publish & kPublishTable) {
       if (start) {
         p.g_expert[gi] = sid;
         p.g_start[gi] = (uint32_t)lane;
         p.g_count[gi] = (uint32_t)(next - lane);
       }
       if (lane == 0) *p.n_groups = (uint32_t)__popcll(mask);
+      // each group's tokens, in sorted-row order, padded with its last (one table read gives
+      // the gate/up workgroup its expert and its activation rows)
+      if (lane < A) {
+        const int g0 = __popcll(mask & ((2ull << lane) - 1ull)) - 1;  // the group of sorted row lane
+        const uint64_t at_or_below = mask & ((2ull << lane) - 1ull);
+        const int first = 63 - __clzll(at_or_below);  // its first sorted row
+        const int i = lane - first;
+        const uint64_t later = lane == 63 ? 0ull : (mask >> (lane + 1));
+        const bool last = lane + 1 == A || (later & 1ull);
+        const uint32_t tok = so_sh[lane] / (uint32_t)p.k;
+        if (i < KM) p.g_tokens[g0 * KM + i] = tok;
+        if (last)
+          for (int j = i + 1; j < KM; ++j) p.g_tokens[g0 * KM + j] = tok;
+      }
     }
   }
   __syncthreads();
-  if (publish) {
+  if (publish & kPublishRoute) {
     // expert offsets [E+2] (E+1: trailing out-of-range bucket, empty here)
     for (int e = threadIdx.x; e <= p.E + 1; e += (int)blockDim.x) {
       uint32_t c = 0;
@@ -438,21 +460,23 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, bool publish, 
   }
 }
 
-// Routing once for a batch of tokens (T >= kDecodeRouteOnceT): one workgroup runs decode_route
-// and publishes it; the gate/up kernel's routed workgroups then read the table instead of
-// each recomputing every token's routing.
+// Routing once for a batch of tokens (T >= kDecodeRouteOnceT): one workgroup computes each
+// token's top-k set (route_token, one wave per token), the distinct-expert table and each
+// group's tokens, and publishes the table; the gate/up kernel's routed workgroups read it
+// instead of each recomputing every token's routing.  The table does not depend on the order
+// within a token's slice (a token selects an expert at most once, so an expert's sorted rows
+// follow its tokens), so the slice in MLX's order -- slow to compute -- is left to a workgroup
+// of the gate/up kernel, beside the GEMVs.
 template <int MT, int PER>
 __global__ __launch_bounds__(64 * MT) void decode_route_kernel(const DecodeArgs p) {
   constexpr int KM = kDecodeMaxK;
-  constexpr int RW = PER >= 16 ? 4 : MT;  // routing waves (LDS: kSelectWords<PER> words each)
   __shared__ uint32_t idx_sh[64], so_sh[64], sid_sh[64];
   __shared__ __attribute__((aligned(16))) uint32_t key_sh[64];
   __shared__ __attribute__((aligned(16))) uint32_t route_sh[MT][KM];
   __shared__ uint16_t sc_sh[64];
   __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
-  __shared__ uint32_t sel_sh[RW * kSelectWords<PER>];
-  decode_route<MT, PER, true>(p, true, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh,
-                              g_count_sh, ng_sh, sel_sh, RW);
+  decode_route<MT, PER, false>(p, kPublishTable, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh,
+                               g_start_sh, g_count_sh, ng_sh);
 }
 
 // Workgroups (x, 0): the shared expert, which needs no routing — x < shared_pair_blocks
@@ -461,11 +485,12 @@ __global__ __launch_bounds__(64 * MT) void decode_route_kernel(const DecodeArgs 
 // expert for every token routed to it (SwiGLU epilogue).  Without PRE (one token) every one
 // of them first recomputes the routing's set from the logits (route_token), the stable sort
 // of the assignments and the table of distinct experts — a few microseconds of one wave's work
-// that saves a dependent kernel boundary — and workgroup (shared_pair_blocks + 1, 0) computes
-// the routing in MLX's slot order (route_token_exact) and publishes it for the down kernel,
-// next to the GEMVs.  With PRE (batches from kDecodeRouteOnceT tokens) decode_route_kernel has
-// published the routing and the workgroups read it instead.  RPW: (gate, up) row pairs per
-// routed wave (more for larger batches: fewer, fuller workgroups).
+// that saves a dependent kernel boundary.  With PRE (batches from kDecodeRouteOnceT tokens)
+// decode_route_kernel has published the table and the workgroups read it instead.  Either way
+// workgroup (shared_pair_blocks + 1, 0) computes the routing in MLX's slot order
+// (route_token_exact, one wave per token up to 4 waves) and publishes it for the down kernel,
+// next to the GEMVs.  RPW: (gate, up) row pairs per routed wave (more for larger batches:
+// fewer, fuller workgroups).
 template <int BITS, int MT, int NC, int PER, bool PRE, int RPW>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p) {
   constexpr int KM = kDecodeMaxK;
@@ -475,12 +500,14 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
   __shared__ uint16_t sc_sh[64];
   __shared__ uint32_t g_expert_sh[64], g_start_sh[64], g_count_sh[64], ng_sh;
   __shared__ int rows_sh[MT], orows_sh[MT];
-  __shared__ uint32_t sel_sh[PRE ? 1 : kSelectWords<PER>];  // the publisher's one routing wave
+  constexpr int PW = MT < 4 ? MT : 4;  // the publisher's routing waves
+  __shared__ uint32_t sel_sh[PW * kSelectWords<PER>];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int nchunks = p.H / 32;
-  if (!PRE && blockIdx.y == 0 && (int)blockIdx.x == p.shared_pair_blocks + 1) {
-    decode_route<MT, PER, true>(p, true, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh,
-                                g_count_sh, ng_sh, sel_sh, 1);
+  if (blockIdx.y == 0 && (int)blockIdx.x == p.shared_pair_blocks + 1) {
+    // (with PRE the table is the routing kernel's, identical and already published)
+    decode_route<MT, PER, true>(p, PRE ? kPublishRoute : kPublishRoute | kPublishTable, idx_sh, so_sh, sid_sh,
+                                key_sh, route_sh, sc_sh, g_expert_sh, g_start_sh, g_count_sh, ng_sh, sel_sh, PW);
     return;
   }
   if (blockIdx.y == 0) {
@@ -523,19 +550,23 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
   if ((int)blockIdx.x * 4 * RPW >= p.I) return;
   uint32_t e, start, m;
   if (PRE) {
+    // the group's table entries, read together with the group count (entries past it are
+    // stale and unused)
     const int g = blockIdx.y - 1;
-    if (g >= (int)*p.n_groups) return;
+    const uint32_t ng = *p.n_groups;
     e = p.g_expert[g];
     start = p.g_start[g];
     m = p.g_count[g];
+    const uint32_t tok = p.g_tokens[g * KM + (threadIdx.x < MT ? threadIdx.x : 0)];
+    if (g >= (int)ng) return;
     if (m > (uint32_t)MT) return;  // a token selects an expert at most once: m <= T <= MT
     if (threadIdx.x < MT) {
       const uint32_t i = threadIdx.x < m ? threadIdx.x : m - 1;
-      rows_sh[threadIdx.x] = (int)(p.sorted_order[start + i] / (uint32_t)p.k);
+      rows_sh[threadIdx.x] = (int)tok;
       orows_sh[threadIdx.x] = (int)(start + i);
     }
   } else {
-    decode_route<MT, PER, false>(p, false, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh,
+    decode_route<MT, PER, false>(p, 0, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh,
                                  g_start_sh, g_count_sh, ng_sh);
     const int g = blockIdx.y - 1;
     if (g >= (int)ng_sh) return;
@@ -572,24 +603,28 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
 
 // ---------------------------------------------------------------- D3: down + combine
 
-// One workgroup of 4 waves per (4 output rows, token).  The token's k experts and the
+// One workgroup of 4 waves per (4 R output rows, token).  The token's k experts and the
 // shared expert are P = kDecodeMaxK + 1 participant rows per output row; wave w computes
-// participants w, w+4, w+8.  Quarter q of a wave (one DPP row of 16 lanes) takes output
-// row 4x + q and its 16 lanes split the input chunks (lane l16 takes chunks l16, l16+16,
-// ...).  The rounded participant values meet in LDS, where wave 0 forms the weighted
-// combine (slot order) and the shared expert's gated add.  Branch-free: participants past
-// k, or a missing shared expert, reuse slot 0's rows and are masked out.
-template <int BITS, int NC, bool SORTED>
+// participants w, w+4, w+8.  Quarter q of a wave (one DPP row of 16 lanes) takes output rows
+// (4x + q) R .. + R and its 16 lanes split the input chunks (lane l16 takes chunks l16,
+// l16+16, ...); a participant's activation chunk is loaded once for its R rows.  The rounded
+// participant values meet in LDS, where wave 0 forms the weighted combine (slot order) and the
+// shared expert's gated add, lane l16 < R of quarter q for row (4x + q) R + l16.  Larger
+// batches take R > 1: fewer, longer workgroups (every workgroup's dependent chain of index
+// and weight loads is paid once per R rows).  Branch-free: participants past k, or a missing
+// shared expert, reuse slot 0's rows and are masked out.
+template <int BITS, int NC, bool SORTED, int R>
 __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   constexpr int KM = kDecodeMaxK, P = KM + 1, PW = (P + 3) / 4;
-  __shared__ float vals[4][4 * PW];
+  __shared__ float vals[4][R][4 * PW];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
-  const int t = blockIdx.y, h = blockIdx.x * 4 + q;
+  const int t = blockIdx.y, h0 = (blockIdx.x * 4 + q) * R;
   const bool has_shared = p.Is > 0;
   // loads the combine needs, issued first (a missing shared expert reads a score instead)
   const uint16_t zbits = has_shared ? p.z[t] : p.scores[0];
-  const uint16_t rbits = p.ffn_out ? p.r_out[(int64_t)t * p.H + h] : 0;  // the decoder step's residual
+  const int hc = h0 + (l16 < R ? l16 : 0);  // this lane's row in the combine
+  const uint16_t rbits = p.ffn_out ? p.r_out[(int64_t)t * p.H + hc] : 0;  // the decoder step's residual
   float sc[KM];
 #pragma unroll
   for (int j = 0; j < KM; ++j) sc[j] = bf2f(p.scores[t * p.k + (j < p.k ? j : p.k - 1)]);
@@ -613,6 +648,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   const uint32_t *wrow[PW];
   const uint16_t *srow[PW], *brow[PW];
   const uint16_t *xrow[PW];
+  int64_t wrs[PW], sbrs[PW];
   int nch[PW], grp[PW];
   uint32_t orow[PW];
   bool live[PW];
@@ -625,28 +661,33 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
     const uint32_t *wb = shared ? sd_w : p.down_w + (int64_t)e[i] * p.dn_w_es;
     const uint16_t *sb = shared ? sd_s : p.down_s + (int64_t)e[i] * p.dn_sb_es;
     const uint16_t *bb = shared ? sd_b : p.down_b + (int64_t)e[i] * p.dn_sb_es;
-    const int64_t wrs = shared ? sd_w_rs : p.dn_w_rs;
-    const int64_t sbrs = shared ? sd_sb_rs : p.dn_sb_rs;
-    wrow[i] = wb + (int64_t)h * wrs;
-    srow[i] = sb + (int64_t)h * sbrs;
-    brow[i] = bb + (int64_t)h * sbrs;
+    wrs[i] = shared ? sd_w_rs : p.dn_w_rs;
+    sbrs[i] = shared ? sd_sb_rs : p.dn_sb_rs;
+    wrow[i] = wb + (int64_t)h0 * wrs[i];
+    srow[i] = sb + (int64_t)h0 * sbrs[i];
+    brow[i] = bb + (int64_t)h0 * sbrs[i];
     xrow[i] = p.act + (int64_t)orow[i] * p.act_ld;
     nch[i] = shared ? sd_nch : p.I / 32;
     grp[i] = shared ? sd_group : p.dn_group;
   }
-  float acc[PW];
+  float acc[PW][R];
 #pragma unroll
-  for (int i = 0; i < PW; ++i) acc[i] = 0.0f;
+  for (int i = 0; i < PW; ++i)
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) acc[i][rr] = 0.0f;
 #pragma unroll
   for (int cc = 0; cc < NC; ++cc) {
     const int craw = l16 + 16 * cc;
     // every load of the chunk step first, then the arithmetic
-    WChunk wch[PW];
+    WChunk wch[PW][R];
     XRaw xr[PW];
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int c = craw < nch[i] ? craw : 0;
-      load_wchunk<BITS>(wch[i], wrow[i], srow[i], brow[i], c, grp[i]);
+#pragma unroll
+      for (int rr = 0; rr < R; ++rr)
+        load_wchunk<BITS>(wch[i][rr], wrow[i] + rr * wrs[i], srow[i] + rr * sbrs[i], brow[i] + rr * sbrs[i], c,
+                          grp[i]);
       load_xraw(xr[i], xrow[i] + c * 32);
     }
     // keep the scheduler from interleaving the first participant's arithmetic (and its
@@ -656,29 +697,34 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
     for (int i = 0; i < PW; ++i) {
       XChunk xc;
       convert_xchunk<BITS>(xc, xr[i]);
-      const float d = chunk_dot<BITS>(wch[i], xc);
-      acc[i] += craw < nch[i] ? d : 0.0f;
+#pragma unroll
+      for (int rr = 0; rr < R; ++rr) {
+        const float d = chunk_dot<BITS>(wch[i][rr], xc);
+        acc[i][rr] += craw < nch[i] ? d : 0.0f;
+      }
     }
   }
 #pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const float v = round_bf(row_sum(acc[i]));
-    if (l16 == 0) {
-      vals[q][wave + 4 * i] = v;
-      if (live[i]) p.down_out[(int64_t)orow[i] * p.H + h] = (uint16_t)f2bf(v);
+  for (int i = 0; i < PW; ++i)
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      const float v = round_bf(row_sum(acc[i][rr]));
+      if (l16 == rr) {
+        vals[q][rr][wave + 4 * i] = v;
+        if (live[i]) p.down_out[(int64_t)orow[i] * p.H + h0 + rr] = (uint16_t)f2bf(v);
+      }
     }
-  }
   __syncthreads();
-  if (wave != 0 || l16 != 0) return;
+  if (wave != 0 || l16 >= R) return;
   float v[KM];
 #pragma unroll
-  for (int j = 0; j < KM; ++j) v[j] = vals[q][j];
+  for (int j = 0; j < KM; ++j) v[j] = vals[q][l16][j];
   const uint32_t sparse = combine_element<SORTED, KM>(v, sc, p.k);
   uint32_t out = sparse;
-  if (has_shared) out = shared_gated_add(sparse, vals[q][KM], round_bf(det_sigmoid(bf2f(zbits))));
-  p.sparse[(int64_t)t * p.H + h] = (uint16_t)sparse;
-  p.y[(int64_t)t * p.H + h] = (uint16_t)out;
-  if (p.ffn_out) p.ffn_out[(int64_t)t * p.H + h] = (uint16_t)f2bf(bf2f(rbits) + bf2f(out));
+  if (has_shared) out = shared_gated_add(sparse, vals[q][l16][KM], round_bf(det_sigmoid(bf2f(zbits))));
+  p.sparse[(int64_t)t * p.H + hc] = (uint16_t)sparse;
+  p.y[(int64_t)t * p.H + hc] = (uint16_t)out;
+  if (p.ffn_out) p.ffn_out[(int64_t)t * p.H + hc] = (uint16_t)f2bf(bf2f(rbits) + bf2f(out));
 }
 
 // 256-thread launch; ev (nullable) = {start, stop} events recorded around the kernel itself
@@ -695,8 +741,7 @@ void launch_gate_up_rpw(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev
   // x: routed row blocks, or the shared expert's pair blocks and its output-gate block
   const int routed_x = (a.I + 4 * RPW - 1) / (4 * RPW);
   // x <= shared_pair_blocks: the shared expert; shared_pair_blocks + 1: the routing publisher
-  // (one token)
-  const int shared_x = a.T < kDecodeRouteOnceT ? a.shared_pair_blocks + 2 : a.Is > 0 ? a.shared_pair_blocks + 1 : 0;
+  const int shared_x = a.shared_pair_blocks + 2;
   const dim3 grid(std::max(routed_x, shared_x), a.max_groups + 1);
   if (a.T >= kDecodeRouteOnceT)
     launch_timed(decode_gate_up_kernel<BITS, MT, NC, PER, true, RPW>, grid, s, ev, a);
@@ -744,15 +789,32 @@ void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev)
   else launch_gate_up_per<BITS, MT, NC, 16>(a, s, ev);
 }
 
-template <int BITS, int NC>
-void launch_down_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  const dim3 grid(a.H / 4, a.T);
+template <int BITS, int NC, int R>
+void launch_down_r(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
+  const dim3 grid(a.H / (4 * R), a.T);
   // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64; a verification
   // window keeps the unsorted one (resident_execution.rs:161-162)
   if (a.A >= 64 && !a.unsorted)
-    launch_timed(decode_down_kernel<BITS, NC, true>, grid, s, ev, a);
+    launch_timed(decode_down_kernel<BITS, NC, true, R>, grid, s, ev, a);
   else
-    launch_timed(decode_down_kernel<BITS, NC, false>, grid, s, ev, a);
+    launch_timed(decode_down_kernel<BITS, NC, false, R>, grid, s, ev, a);
+}
+
+template <int BITS, int NC>
+void launch_down_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
+  // output rows per quarter-wave by batch size (H is a multiple of 32, so 4 R divides it);
+  // longer rows keep one row per quarter and 8-bit codes at most two (their code registers)
+  const int r = a.T <= kDecodeDownR1T ? 1 : a.T <= kDecodeDownR2T ? 2 : 4;
+  if constexpr (NC > 1) {
+    launch_down_r<BITS, NC, 1>(a, s, ev);
+  } else if constexpr (BITS == 8) {
+    if (r == 1) launch_down_r<BITS, NC, 1>(a, s, ev);
+    else launch_down_r<BITS, NC, 2>(a, s, ev);
+  } else {
+    if (r == 1) launch_down_r<BITS, NC, 1>(a, s, ev);
+    else if (r == 2) launch_down_r<BITS, NC, 2>(a, s, ev);
+    else launch_down_r<BITS, NC, 4>(a, s, ev);
+  }
 }
 
 template <int BITS, int MT>

@@ -173,6 +173,7 @@ struct DecodeArgs {
   uint16_t *logits, *scores;
   uint32_t *idx, *sorted_order, *inverse_order, *sorted_ids, *offsets;
   uint32_t *n_groups, *g_expert, *g_start, *g_count;
+  uint32_t *g_tokens;  // [64][kDecodeMaxK]: the tokens of group g's sorted rows (the last repeated)
   uint16_t *act, *down_out, *z;
   int64_t act_ld;
   uint16_t *sparse, *y;  // outputs: weighted sum of the routed experts, block output
@@ -196,6 +197,12 @@ constexpr int kDecodeRowsPerWave = 1;  // must match kRowsPerWave in decode.hip
 // gate/up workgroup recomputing every token's routing
 constexpr int kDecodeRouteOnceT = 2;
 constexpr int kDecodeMaxK = 8;         // experts per token the decode combine unrolls
+// the down kernel's output rows per quarter-wave: 1 up to kDecodeDownR1T tokens, 2 up to
+// kDecodeDownR2T, then 4
+constexpr int kDecodeDownR1T = 1;
+constexpr int kDecodeDownR2T = 2;
+// tokens per pass of a gate/up wave of several row pairs (fewer registers, more waves per SIMD)
+constexpr int kDecodePassTokens = 2;
 // launches the decode kernels (router | [routing, T >= kDecodeRouteOnceT] | shared gate/up +
 // routing (T = 1) + routed gate/up | down + combine); kev (nullable) = start/stop event pairs
 // recorded around the router, gate/up and down kernels, and (kev[6..7]) the routing kernel
