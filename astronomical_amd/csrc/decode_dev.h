@@ -565,6 +565,25 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
       rows_sh[threadIdx.x] = (int)tok;
       orows_sh[threadIdx.x] = (int)(start + i);
     }
+  } else if constexpr (MT == 1) {
+    // one token: its k experts are the k groups, in ascending id order, each one row (row g,
+    // token 0).  Wave 0 computes the set (route_set8: no slot order, scores or sort table) and
+    // passes the workgroup's expert on through one LDS word; the other waves wait at the barrier
+    // (routing in every wave would crowd the SIMDs' other waves).
+    const int g = blockIdx.y - 1;
+    if (g >= p.k) return;
+    if (wave == 0) {
+      uint32_t ids[8];
+      route_set8<PER>(p.logits, p.E, p.k, ids);
+      uint32_t eg = ids[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) eg = g == i ? ids[i] : eg;
+      if ((threadIdx.x & 63) == 0) g_expert_sh[0] = eg;
+    }
+    __syncthreads();
+    e = g_expert_sh[0];
+    start = (uint32_t)g;
+    m = 1;
   } else {
     decode_route<MT, PER, false>(p, 0, idx_sh, so_sh, sid_sh, key_sh, route_sh, sc_sh, g_expert_sh,
                                  g_start_sh, g_count_sh, ng_sh);
@@ -580,7 +599,10 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
       orows_sh[threadIdx.x] = (int)(start + i);
     }
   }
-  __syncthreads();
+  const int xrow0 = 0, orow0 = (int)start;  // the single-token path's row and output row
+  constexpr bool kOne = !PRE && MT == 1;
+  if (!kOne) __syncthreads();
+  const int *xrows = kOne ? &xrow0 : rows_sh, *orows = kOne ? &orow0 : orows_sh;
   const int r0 = (blockIdx.x * 4 + wave) * RPW;
   if (r0 >= p.I) return;
   const int nrows = min(RPW, p.I - r0);
@@ -592,8 +614,8 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
     constexpr int M2 = decltype(mt_tag)::value;
     rows_task_q<BITS, M2, RPW, true, NC>(p.gate_w + wo, p.gate_s + so, p.gate_b + so, p.up_w + wo,
                                                 p.up_s + so, p.up_b + so, p.gu_w_rs, p.gu_sb_rs, nrows, nchunks,
-                                                p.gu_group, p.x, p.H, rows_sh, (int)m, p.act + r0, p.act_ld,
-                                                orows_sh);
+                                                p.gu_group, p.x, p.H, xrows, (int)m, p.act + r0, p.act_ld,
+                                                orows);
   };
   if (m <= 1) routed_rows(std::integral_constant<int, 1>());
   else if (MT > 2 && m <= 2) routed_rows(std::integral_constant<int, (MT > 2 ? 2 : MT)>());

@@ -108,6 +108,90 @@ __device__ __forceinline__ void route_token(const uint16_t *__restrict__ l, int 
   out_score = route_scores<KMAX>(my_key >> 16, k, normalize, sh);
 }
 
+// The 8 largest keys of a wave, descending, in every lane (uniform values): each lane's list of
+// its 8 largest keys (descending; 0 pads), then six bitonic merges with a partner lane's list
+// fetched by DPP -- lane ^ 1, lane ^ 2 (quads), row rotations by 4 and 8 (rows), then row 15's
+// list into rows 1 and 3 and row 31's into rows 2 and 3 -- after which lane 63 holds the wave's
+// 8 largest.  A merge keeps the top 8 of two descending lists a, b: c_i = max(a_i, b_{7-i}) is a
+// bitonic sequence holding them, sorted by three half-cleaner stages.  Partner lists are
+// disjoint at every level (rows not written by a broadcast merge zeros, the identity), so no
+// key is counted twice.  Each level is 8 DPP moves and 32 independent min/max: a few hundred
+// cycles in all, against k dependent rounds of a wave-wide maximum.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void top8_merge(uint32_t (&a)[8]) {
+  uint32_t b[8], c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) b[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a[i], CTRL, ROWS, 0xf, false);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = max(a[i], b[7 - i]);
+#pragma unroll
+  for (int d = 4; d >= 1; d >>= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if ((i & d) == 0) {
+        const uint32_t hi = max(c[i], c[i + d]), lo = min(c[i], c[i + d]);
+        c[i] = hi;
+        c[i + d] = lo;
+      }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = c[i];
+}
+
+// keys: this lane's PER keys (0 = empty), descending.  Returns the wave's 8 largest keys,
+// descending, uniform.
+template <int PER>
+__device__ __forceinline__ void wave_top8(const uint32_t (&keys)[PER], uint32_t (&top)[8]) {
+  uint32_t a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = i < PER ? keys[i] : 0u;
+  top8_merge<0xb1, 0xf>(a);   // lane ^ 1
+  top8_merge<0x4e, 0xf>(a);   // lane ^ 2
+  top8_merge<0x124, 0xf>(a);  // row_ror:4
+  top8_merge<0x128, 0xf>(a);  // row_ror:8: the row's 8 largest in every lane of the row
+  top8_merge<0x142, 0xa>(a);  // row_bcast:15 into rows 1 and 3
+  top8_merge<0x143, 0xc>(a);  // row_bcast:31 into rows 2 and 3: lane 63 holds the wave's
+#pragma unroll
+  for (int i = 0; i < 8; ++i) top[i] = (uint32_t)__builtin_amdgcn_readlane((int)a[i], 63);
+}
+
+// The top-k SET of one token (k <= 8) with no slot order and no scores: its expert ids in
+// ascending id order in ids[0, k) (0xffffffff past k), uniform.  The keys and their order are
+// route_token's, so the set is the same.
+template <int PER>
+__device__ __forceinline__ void route_set8(const uint16_t *__restrict__ l, int E, int k, uint32_t (&ids)[8]) {
+  const int lane = (int)(threadIdx.x & 63);
+  uint32_t pb[PER];
+  route_probabilities<PER>(l, E, pb);
+  uint32_t cand[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    cand[i] = e < E ? ((pb[i] << 16) | (uint32_t)e) + 1u : 0u;
+  }
+  // per-lane descending order (odd-even transposition network)
+#pragma unroll
+  for (int pass = 0; pass < PER; ++pass)
+#pragma unroll
+    for (int i = pass & 1; i + 1 < PER; i += 2) {
+      const uint32_t hi = max(cand[i], cand[i + 1]), lo = min(cand[i], cand[i + 1]);
+      cand[i] = hi;
+      cand[i + 1] = lo;
+    }
+  uint32_t top[8];
+  wave_top8<PER>(cand, top);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ids[i] = i < k ? (top[i] - 1u) & 0xffffu : 0xffffffffu;
+  // ascending ids: odd-even transposition over the 8 uniform values
+#pragma unroll
+  for (int pass = 0; pass < 8; ++pass)
+#pragma unroll
+    for (int i = pass & 1; i + 1 < 8; i += 2) {
+      const uint32_t lo = min(ids[i], ids[i + 1]), hi = max(ids[i], ids[i + 1]);
+      ids[i] = lo;
+      ids[i + 1] = hi;
+    }
+}
+
 // ------------------------------------------------------------------ MLX CPU argpartition order
 //
 // MLX's CPU argpartition (the oracle the reference's routing is checked against) fills an

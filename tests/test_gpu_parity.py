@@ -367,6 +367,22 @@ def test_block_c1_decode(ops, orc, c1_layer, T):
     _check_block(ops, orc, c1_layer, S.make_tokens(CF.C1, T), f"c1 B={T}")
 
 
+@pytest.mark.parametrize("group", [2, 3, 5])
+def test_block_c1_decode_tied_router_rows(ops, orc, c1_layer, group):
+    """Router rows repeated in runs of `group` experts: those experts' logits and bf16
+    probabilities are equal, so the top-k set and its order rest on the index tie rule (ties
+    toward the higher index) in every routing path the decode kernels take -- the single-token
+    set of the gate/up workgroups, the batch routing kernel and the published MLX order."""
+    import copy
+    L = copy.copy(c1_layer)
+    w = np.array(c1_layer.router_w, copy=True)
+    w[:] = w[(np.arange(w.shape[0]) // group) * group]
+    L.router_w = w
+    for i, T in enumerate((1, 1, 1, 2, 8)):
+        x = S.make_tokens(CF.C1, T, step=100 * group + i)
+        _check_block(ops, orc, L, x, f"c1 tied rows x{group} B={T}")
+
+
 @pytest.fixture(scope="module")
 def c1_affine_router_layers():
     return {bits: S.make_layer(CF.C1, router_bits=bits) for bits in (4, 8)}
