@@ -401,7 +401,7 @@ __device__ __forceinline__ int hoare_step(uint32_t *a, uint32_t *pg, uint32_t *p
 
 // std::nth_element(a, a + nth, a + n) over the unique keys a[0, n) in LDS, as libstdc++ runs
 // it (see above).  One wave; n <= 64 * PER; pg and pl hold 32 * PER words each, spare 64.
-// Ranges of at most 65 positions (most of the steps) take the one-chunk partition.  The heap
+// Each step partitions in as many 64-position chunks as its range needs.  The heap
 // selection (reached only after 2 floor(log2 n) unbalanced partitions, i.e. adversarial keys)
 // runs on one lane.
 template <int PER>
@@ -437,8 +437,13 @@ __device__ __forceinline__ void nth_element_wave(uint32_t *a, uint32_t *pg, uint
       return;
     }
     --depth;
-    const int cut = PER == 1 || l - f <= 65 ? hoare_step<1>(a, pg, pl, spare, f, l)
-                                            : hoare_step<PER>(a, pg, pl, spare, f, l);
+    // as many 64-position chunks as [f + 1, l) needs (a step's ballots and moves run per chunk)
+    const int len = l - f;
+    constexpr int C2 = PER < 2 ? PER : 2, C4 = PER < 4 ? PER : 4;
+    const int cut = len <= 65 ? hoare_step<1>(a, pg, pl, spare, f, l)
+                    : len <= 129 ? hoare_step<C2>(a, pg, pl, spare, f, l)
+                    : len <= 257 ? hoare_step<C4>(a, pg, pl, spare, f, l)
+                                 : hoare_step<PER>(a, pg, pl, spare, f, l);
     if (cut <= nth) f = cut;
     else l = cut;
   }
