@@ -358,9 +358,9 @@ constexpr int kPublishRoute = 1, kPublishTable = 2;
 // the table of distinct experts, into LDS; publish (kPublish* bits) selects what is also written
 // to the workspace for the later kernels.  EXACT: each token's slice in the order of MLX's CPU
 // argpartition (route_token_exact; waves 0 .. route_waves - 1 route, each with
-// kSelectWords<PER> words of sel_sh); otherwise the slice in ascending key order (route_token),
-// which gives the same set, hence the same distinct-expert table and rows per expert, but not
-// the same slot order -- enough for the table, not for the routing.
+// kSelectWords<PER> words of sel_sh); otherwise the set in ascending id order with no scores
+// (route_set8), which gives the same distinct-expert table and rows per expert, but not the
+// same slot order -- enough for the table (kPublishTable), not for the routing (kPublishRoute).
 template <int MT, int PER, bool EXACT>
 __device__ __forceinline__ void decode_route(const DecodeArgs &p, int publish, uint32_t *idx_sh, uint32_t *so_sh,
                                              uint32_t *sid_sh, uint32_t *key_sh, uint32_t (*route_sh)[kDecodeMaxK],
@@ -377,7 +377,13 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, int publish, u
       route_token_exact<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize,
                                  sel_sh + wave * kSelectWords<PER>, route_sh[wave], my_idx, my_score);
     } else {
-      route_token<PER, KM>(p.logits + (int64_t)t * p.E, p.E, p.k, p.normalize, route_sh[wave], my_idx, my_score);
+      // the set only (the table needs no order and no scores): ascending ids
+      uint32_t ids[8];
+      route_set8<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, ids);
+      my_idx = ids[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) my_idx = lane == i ? ids[i] : my_idx;
+      my_score = 0;
     }
     if (lane < p.k) {
       idx_sh[t * p.k + lane] = my_idx;
@@ -482,10 +488,11 @@ __global__ __launch_bounds__(64 * MT) void decode_route_kernel(const DecodeArgs 
 // Workgroups (x, 0): the shared expert, which needs no routing — x < shared_pair_blocks
 // computes 4 (gate row, up row) pairs with the SwiGLU epilogue, x == shared_pair_blocks
 // the output gate z.  Workgroups (x, g + 1): rows of the gate/up GEMV of the g-th distinct
-// expert for every token routed to it (SwiGLU epilogue).  Without PRE (one token) every one
-// of them first recomputes the routing's set from the logits (route_token), the stable sort
-// of the assignments and the table of distinct experts — a few microseconds of one wave's work
-// that saves a dependent kernel boundary.  With PRE (batches from kDecodeRouteOnceT tokens)
+// expert for every token routed to it (SwiGLU epilogue).  Without PRE (fewer than
+// kDecodeRouteOnceT tokens) every one of them first recomputes the routing's set from the
+// logits (route_set8; with two tokens, one wave each, then the stable sort of the assignments
+// and the table of distinct experts) — a few microseconds of one wave's work that saves a
+// dependent kernel boundary.  With PRE (batches from kDecodeRouteOnceT tokens)
 // decode_route_kernel has published the table and the workgroups read it instead.  Either way
 // workgroup (shared_pair_blocks + 1, 0) computes the routing in MLX's slot order
 // (route_token_exact, one wave per token up to 4 waves) and publishes it for the down kernel,

@@ -194,8 +194,9 @@ constexpr int kDecodeStepLds = 60 * 1024;
 bool decode_supported(const DecodeArgs &a);
 constexpr int kDecodeRowsPerWave = 1;  // must match kRowsPerWave in decode.hip
 // from this many tokens a one-workgroup kernel routes the batch once, instead of every routed
-// gate/up workgroup recomputing every token's routing
-constexpr int kDecodeRouteOnceT = 2;
+// gate/up workgroup recomputing every token's top-k set (one wave per token; c1: B = 2 23.6 us
+// per layer in-workgroup against 24.3 with the routing kernel, B = 4 33.7 against 33.1)
+constexpr int kDecodeRouteOnceT = 3;
 constexpr int kDecodeMaxK = 8;         // experts per token the decode combine unrolls
 // the down kernel's output rows per quarter-wave: 1 up to kDecodeDownR1T tokens, 2 up to
 // kDecodeDownR2T, then 4
