@@ -91,6 +91,30 @@ __device__ __forceinline__ float sigmoid_bf(float g) {
   return round_bf(s);
 }
 
+// inputs (0, 4), (1, 5), (2, 6), (3, 7) of 8 consecutive bf16 values: the pairing of the
+// exact-code GEMM's 4-bit unpack
+__device__ __forceinline__ u32x4 pair_code_order(const u32x4 &d) {
+  u32x4 a;
+  a[0] = (d[0] & 0xffffu) | (d[2] << 16);
+  a[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
+  a[2] = (d[1] & 0xffffu) | (d[3] << 16);
+  a[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
+  return a;
+}
+
+// The fp32 sum of the g inputs at src (g / 8 pieces of 8 bf16), in input order: one group's
+// sum for the exact-code GEMM's affine terms; with dst, also the inputs in the codes' pairing.
+__device__ __forceinline__ float group_sum_paired(const u32x4 *src, int g, u32x4 *dst) {
+  float sum = 0.0f;
+  for (int c = 0; c < g / 8; ++c) {
+    const u32x4 v = src[c];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) sum = (sum + bf_lo(v[w])) + bf_hi(v[w]);
+    if (dst) dst[c] = pair_code_order(v);
+  }
+  return sum;
+}
+
 // SwiGLU with the reference's three bf16 roundings (mlx_compiled_swiglu.rs:66-86):
 // s = bf16(sigmoid(g)); a = bf16(g*s); out = bf16(a*u).
 __device__ __forceinline__ uint32_t swiglu_bf(float g, float u) {

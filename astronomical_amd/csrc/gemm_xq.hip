@@ -78,16 +78,6 @@ __device__ __forceinline__ u32x4 xq_unpack(uint32_t w, uint32_t mask, uint32_t k
   return r;
 }
 
-// inputs (0, 4), (1, 5), (2, 6), (3, 7) of 8 consecutive bf16 values: the codes' pairing
-__device__ __forceinline__ u32x4 xq_pair(const u32x4 &d) {
-  u32x4 a;
-  a[0] = (d[0] & 0xffffu) | (d[2] << 16);
-  a[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
-  a[2] = (d[1] & 0xffffu) | (d[3] << 16);
-  a[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
-  return a;
-}
-
 // place of input e of an 8-input chunk in the codes' pairing (0 4 1 5 2 6 3 7)
 __device__ __forceinline__ int xq_pair_pos(int col) { return (col & ~7) | ((col & 3) << 1) | ((col >> 2) & 1); }
 
@@ -505,14 +495,7 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t *__restr
   const int r = (int)(i / G), gi = (int)(i - (int64_t)r * G);
   const u32x4 *src = (const u32x4 *)(A + (int64_t)r * lda + (int64_t)gi * g);
   u32x4 *dst = paired ? (u32x4 *)(paired + (int64_t)r * K + (int64_t)gi * g) : nullptr;
-  float sum = 0.0f;
-  for (int c = 0; c < g / 8; ++c) {
-    const u32x4 v = src[c];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) sum = (sum + bf_lo(v[w])) + bf_hi(v[w]);
-    if (dst) dst[c] = xq_pair(v);
-  }
-  X[(int64_t)r * ldx + gi] = sum;
+  X[(int64_t)r * ldx + gi] = group_sum_paired(src, g, dst);
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }

@@ -84,8 +84,17 @@ hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilog
 bool affine_rows_supported(const GemmArgs &a, int epilogue);
 hipError_t launch_affine_rows(const GemmArgs &a, int epilogue, hipStream_t s);
 
+// x's group sums and paired copy written by the route kernel (the exact-code gate/up's inputs,
+// as launch_group_sums writes them for rows of H inputs in groups of g); x null: not written
+struct RouteGroupSums {
+  const uint16_t *x = nullptr;
+  int H = 0, g = 0;
+  float *xsum = nullptr;     // [T][H / g]
+  uint16_t *paired = nullptr;  // [T][H]
+};
 hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
-                             uint32_t *idx, uint16_t *scores, hipStream_t s);
+                             uint32_t *idx, uint16_t *scores, hipStream_t s,
+                             const RouteGroupSums &gs = RouteGroupSums());
 
 // counting sort of assignment ids by expert (stable), plus the grouped-GEMM tile table
 // (tiles of kGemmBM rows).  offsets has E+2 entries (ids >= E land in a trailing

@@ -9,12 +9,14 @@ namespace astro {
 namespace {
 
 // One wave per token (route_token_exact in route_dev.h: the slice in the order MLX's CPU
-// argpartition leaves it).
+// argpartition leaves it).  With gs.x set, the wave also writes its token's group sums and
+// paired copy (group_sums_kernel's work, one lane per group, the same order of additions): the
+// exact-code gate/up's inputs, which then need no launch of their own.
 template <int PER, int KMAX>
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restrict__ logits,
                                                          int T, int E, int k, int normalize,
                                                          uint32_t *__restrict__ idx,
-                                                         uint16_t *__restrict__ scores) {
+                                                         uint16_t *__restrict__ scores, const RouteGroupSums gs) {
   __shared__ __attribute__((aligned(16))) uint32_t sh[4][KMAX];
   __shared__ uint32_t sel[4][kSelectWords<PER>];  // per wave: keys, the partition's pair tables
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -25,6 +27,14 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restr
   if (lane < k) {
     idx[(int64_t)t * k + lane] = my_idx;
     scores[(int64_t)t * k + lane] = (uint16_t)my_score;
+  }
+  if (gs.x) {
+    const int G = gs.H / gs.g;
+    for (int gi = lane; gi < G; gi += 64) {
+      const u32x4 *src = (const u32x4 *)(gs.x + (int64_t)t * gs.H + (int64_t)gi * gs.g);
+      u32x4 *dst = (u32x4 *)(gs.paired + (int64_t)t * gs.H + (int64_t)gi * gs.g);
+      gs.xsum[(int64_t)t * G + gi] = group_sum_paired(src, gs.g, dst);
+    }
   }
 }
 
@@ -215,28 +225,29 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
 
 template <int KMAX>
 void launch_route_k(const uint16_t *logits, int T, int E, int k, int normalize, uint32_t *idx,
-                    uint16_t *scores, hipStream_t s) {
+                    uint16_t *scores, hipStream_t s, const RouteGroupSums &gs) {
   const dim3 grid((T + 3) / 4), block(256);
   const int per = (E + 63) / 64;
   if (per <= 1)
-    hipLaunchKernelGGL((route_topk_kernel<1, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<1, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
   else if (per <= 2)
-    hipLaunchKernelGGL((route_topk_kernel<2, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<2, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
   else if (per <= 4)
-    hipLaunchKernelGGL((route_topk_kernel<4, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<4, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
   else if (per <= 8)
-    hipLaunchKernelGGL((route_topk_kernel<8, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<8, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
   else
-    hipLaunchKernelGGL((route_topk_kernel<16, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores);
+    hipLaunchKernelGGL((route_topk_kernel<16, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
 }
 
 hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
-                             uint32_t *idx, uint16_t *scores, hipStream_t s) {
+                             uint32_t *idx, uint16_t *scores, hipStream_t s, const RouteGroupSums &gs) {
   if (T <= 0) return hipSuccess;
+  if (gs.x && (gs.g <= 0 || gs.g % 8 || gs.H % gs.g || !gs.xsum || !gs.paired)) return hipErrorInvalidValue;
   // KMAX bounds the renormalisation's unrolled slice sum
-  if (k <= 8) launch_route_k<8>(logits, T, E, k, normalize, idx, scores, s);
-  else if (k <= 16) launch_route_k<16>(logits, T, E, k, normalize, idx, scores, s);
-  else launch_route_k<64>(logits, T, E, k, normalize, idx, scores, s);
+  if (k <= 8) launch_route_k<8>(logits, T, E, k, normalize, idx, scores, s, gs);
+  else if (k <= 16) launch_route_k<16>(logits, T, E, k, normalize, idx, scores, s, gs);
+  else launch_route_k<64>(logits, T, E, k, normalize, idx, scores, s, gs);
   return hipGetLastError();
 }
 
