@@ -452,7 +452,8 @@ SparsePlan plan_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int k
 
 hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk, const uint32_t *ids,
                       const uint16_t *scores, const Layout &o, char *ws, bool with_shared, uint16_t *y,
-                      hipStream_t s, StageClock *clock, bool force_unsorted = false, bool sums_ready = false) {
+                      hipStream_t s, StageClock *clock, bool force_unsorted = false, bool sums_ready = false,
+                      bool gate_ready = false) {
   auto at = [&](size_t off) { return (void *)(ws + off); };
   auto begin = [&](int i) {
     if (clock) clock->begin(i);
@@ -474,7 +475,7 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
 
   // the sort stage also takes x's group sums and paired copy (the exact-code gate/up's
   // inputs), so the gate/up stage is the one GEMM launch; sums_ready: the route kernel has
-  // written them
+  // written them (gate_ready: and the shared expert's output gate z)
   begin(2);
   hipError_t e = launch_sort(ids, A, E, (uint32_t *)at(o.sorted_order), inverse, (uint32_t *)at(o.sorted_ids),
                              (uint32_t *)at(o.offsets), (uint32_t *)at(o.tile_expert), (uint32_t *)at(o.tile_row0),
@@ -496,7 +497,7 @@ hipError_t run_sparse(const astro_moe_layer &L, const uint16_t *x, int T, int kk
     e = has_shared ? launch_grouped_gemm2(sdn, &dn, kEpiPlain, s) : launch_grouped_gemm2(dn, nullptr, kEpiPlain, s);
   end(4);
 
-  if (has_shared) {
+  if (has_shared && !gate_ready) {
     begin(5);
     if (e == hipSuccess) e = run_shared_gate(L, x, T, z, s);
     end(5);
@@ -693,18 +694,32 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   hipError_t e = run_router(L, x, T, logits, s);
   end(0);
   begin(1);
-  // the route kernel also writes x's group sums and paired copy when the sorted path's gate/up
-  // takes them (run_sparse's plan, which only reads the layer and the layout)
-  RouteGroupSums gs;
-  if (plan_sparse(L, x, T, k, o, ws, true).paired_x && ((uintptr_t)x & 15) == 0) {
-    const astro_moe_affine &gu_w = L.gate_up.w ? L.gate_up : L.gate;
-    gs.x = x;
-    gs.H = H;
-    gs.g = gu_w.group_size;
-    gs.xsum = (float *)at(o.xsum_x);
-    gs.paired = (uint16_t *)at(o.xpair);
+  // the route kernel's wave per token also writes x's group sums and paired copy when the
+  // sorted path's gate/up takes them (run_sparse's plan, which only reads the layer and the
+  // layout) and the shared expert's output gate z (run_shared_gate's qgemv rows)
+  RouteExtras ex;
+  if (((uintptr_t)x & 15) == 0 && H % 32 == 0) {
+    if (plan_sparse(L, x, T, k, o, ws, true).paired_x) {
+      const astro_moe_affine &gu_w = L.gate_up.w ? L.gate_up : L.gate;
+      ex.x = x;
+      ex.H = H;
+      ex.g = gu_w.group_size;
+      ex.xsum = (float *)at(o.xsum_x);
+      ex.paired = (uint16_t *)at(o.xpair);
+    }
+    const astro_moe_affine &zg = L.shared_expert_gate;
+    if (has_shared && (zg.bits == 4 || zg.bits == 8) && zg.group_size % 32 == 0) {
+      ex.x = x;
+      ex.H = H;
+      ex.zw = zg.w;
+      ex.zs = zg.scales;
+      ex.zb = zg.biases;
+      ex.zbits = zg.bits;
+      ex.zgroup = zg.group_size;
+      ex.z = z;
+    }
   }
-  if (e == hipSuccess) e = launch_route_topk(logits, T, E, k, L.normalize_top_k, idx, scores, s, gs);
+  if (e == hipSuccess) e = launch_route_topk(logits, T, E, k, L.normalize_top_k, idx, scores, s, ex);
   // compact pages (forward_moe_paged, paged_execution.rs:98-139): the expert ids become page
   // slots (qwen3_5_moe_remap_expert_page_slots, split_page_route.rs:79-105) before the sort
   const uint32_t *ids = idx;
@@ -718,7 +733,8 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
   // a verification window keeps the unsorted reduction at every length
   // (forward_moe_resident_target_verification, resident_execution.rs:146-208)
-  e = run_sparse(L, x, T, k, ids, scores, o, ws, true, y, s, clock, verification, gs.x != nullptr);
+  e = run_sparse(L, x, T, k, ids, scores, o, ws, true, y, s, clock, verification, ex.xsum != nullptr,
+                 ex.z != nullptr);
   if (e != hipSuccess) return hip_fail(kBlockOp, e);
   return finish();
 }

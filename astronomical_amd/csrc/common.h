@@ -263,6 +263,40 @@ __device__ __forceinline__ float wave_sum_fast(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// One affine row (BITS-bit codes, one bf16 scale and bias per group) times one bf16 input row
+// of K (a multiple of 32) on one wave: lane l covers inputs 32l.. of each 2048-wide chunk,
+// dequantising in fp32 (scale*q + bias) and accumulating x*w with fma; the wave sum in every
+// lane.
+template <int BITS>
+__device__ __forceinline__ float qgemv_row_wave(const uint16_t *__restrict__ xr, int K, const uint32_t *__restrict__ wr,
+                                                const uint16_t *__restrict__ sr, const uint16_t *__restrict__ br,
+                                                int group) {
+  const int lane = threadIdx.x & 63;
+  float acc = 0.f;
+  for (int k0 = lane * 32; k0 < K; k0 += 64 * 32) {
+    const float s = bf2f(sr[k0 / group]), b = bf2f(br[k0 / group]);
+    const u32x4 *xp = (const u32x4 *)(xr + k0);
+    float xv[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 q = xp[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xv[8 * c + 2 * i] = bf_lo(q[i]);
+        xv[8 * c + 2 * i + 1] = bf_hi(q[i]);
+      }
+    }
+    const uint32_t *wp = wr + k0 * BITS / 32;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t word = wp[i * BITS / 32];
+      const float q = (float)((word >> ((i * BITS) & 31)) & ((1u << BITS) - 1u));
+      acc = __builtin_fmaf(xv[i], __builtin_fmaf(s, q, b), acc);
+    }
+  }
+  return wave_sum_fast(acc);
+}
+
 // Maximum over the wave of unsigned keys with DPP only (quad permutes, row rotations, then
 // row_bcast:15 / row_bcast:31 fold the rows into lane 63) and one readlane: a single
 // vector-to-scalar transfer.  Uniform result.

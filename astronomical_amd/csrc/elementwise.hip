@@ -132,8 +132,7 @@ __global__ __launch_bounds__(256) void combine_shared_kernel(
   y[i] = (uint16_t)f2bf(bf2f(sparse[i]) + round_bf(bf2f(shared_out[i]) * gate));
 }
 
-// One wave per (token, output row): lane l covers inputs 32l.. of each 2048-wide chunk,
-// dequantising in fp32 (scale*q + bias) and accumulating x*w with fma; wave sum.
+// One wave per (token, output row) (qgemv_row_wave).
 template <int BITS>
 __global__ __launch_bounds__(256) void qgemv_rows_kernel(
     const uint16_t *__restrict__ x, int T, int K, const uint32_t *__restrict__ w,
@@ -143,34 +142,8 @@ __global__ __launch_bounds__(256) void qgemv_rows_kernel(
   const int item = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (item >= T * N) return;
   const int t = item / N, n = item % N;
-  const int wpr = K * BITS / 32;          // words per row
-  const uint32_t *wr = w + (int64_t)n * wpr;
-  const uint16_t *sr = sc + (int64_t)n * (K / group);
-  const uint16_t *br = bi + (int64_t)n * (K / group);
-  const uint16_t *xr = x + (int64_t)t * K;
-  float acc = 0.f;
-  for (int k0 = lane * 32; k0 < K; k0 += 64 * 32) {
-    const float s = bf2f(sr[k0 / group]), b = bf2f(br[k0 / group]);
-    const u32x4 *xp = (const u32x4 *)(xr + k0);
-    float xv[32];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const u32x4 q = xp[c];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        xv[8 * c + 2 * i] = bf_lo(q[i]);
-        xv[8 * c + 2 * i + 1] = bf_hi(q[i]);
-      }
-    }
-    const uint32_t *wp = wr + k0 * BITS / 32;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const uint32_t word = wp[i * BITS / 32];
-      const float q = (float)((word >> ((i * BITS) & 31)) & ((1u << BITS) - 1u));
-      acc = __builtin_fmaf(xv[i], __builtin_fmaf(s, q, b), acc);
-    }
-  }
-  acc = wave_sum_fast(acc);
+  const float acc = qgemv_row_wave<BITS>(x + (int64_t)t * K, K, w + (int64_t)n * (K * BITS / 32),
+                                         sc + (int64_t)n * (K / group), bi + (int64_t)n * (K / group), group);
   if (lane == 0) out[(int64_t)t * N + n] = (uint16_t)f2bf(acc);
 }
 

@@ -84,17 +84,23 @@ hipError_t launch_grouped_gemm2(const GemmArgs &a, const GemmArgs *b, int epilog
 bool affine_rows_supported(const GemmArgs &a, int epilogue);
 hipError_t launch_affine_rows(const GemmArgs &a, int epilogue, hipStream_t s);
 
-// x's group sums and paired copy written by the route kernel (the exact-code gate/up's inputs,
-// as launch_group_sums writes them for rows of H inputs in groups of g); x null: not written
-struct RouteGroupSums {
+// Work on the token rows x (T rows of H) that the route kernel's wave per token also does:
+// x's group sums and paired copy (the exact-code gate/up's inputs, as launch_group_sums writes
+// them, groups of g; xsum null: not written) and the shared expert's output gate z (one affine
+// row, as launch_qgemv_rows computes it; z null: not computed).  x null: neither.
+struct RouteExtras {
   const uint16_t *x = nullptr;
   int H = 0, g = 0;
-  float *xsum = nullptr;     // [T][H / g]
+  float *xsum = nullptr;       // [T][H / g]
   uint16_t *paired = nullptr;  // [T][H]
+  const uint32_t *zw = nullptr;
+  const uint16_t *zs = nullptr, *zb = nullptr;
+  int zbits = 0, zgroup = 0;
+  uint16_t *z = nullptr;       // [T]
 };
 hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
                              uint32_t *idx, uint16_t *scores, hipStream_t s,
-                             const RouteGroupSums &gs = RouteGroupSums());
+                             const RouteExtras &ex = RouteExtras());
 
 // counting sort of assignment ids by expert (stable), plus the grouped-GEMM tile table
 // (tiles of kGemmBM rows).  offsets has E+2 entries (ids >= E land in a trailing

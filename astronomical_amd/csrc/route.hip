@@ -9,14 +9,15 @@ namespace astro {
 namespace {
 
 // One wave per token (route_token_exact in route_dev.h: the slice in the order MLX's CPU
-// argpartition leaves it).  With gs.x set, the wave also writes its token's group sums and
-// paired copy (group_sums_kernel's work, one lane per group, the same order of additions): the
-// exact-code gate/up's inputs, which then need no launch of their own.
+// argpartition leaves it).  With ex.x set, the wave also does the token's share of the work
+// RouteExtras lists: its group sums and paired copy (group_sums_kernel's work, one lane per
+// group, the same order of additions) and its shared-expert gate (qgemv_row_wave, as
+// qgemv_rows_kernel), which then need no launches of their own.
 template <int PER, int KMAX>
 __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restrict__ logits,
                                                          int T, int E, int k, int normalize,
                                                          uint32_t *__restrict__ idx,
-                                                         uint16_t *__restrict__ scores, const RouteGroupSums gs) {
+                                                         uint16_t *__restrict__ scores, const RouteExtras ex) {
   __shared__ __attribute__((aligned(16))) uint32_t sh[4][KMAX];
   __shared__ uint32_t sel[4][kSelectWords<PER>];  // per wave: keys, the partition's pair tables
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -28,12 +29,18 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restr
     idx[(int64_t)t * k + lane] = my_idx;
     scores[(int64_t)t * k + lane] = (uint16_t)my_score;
   }
-  if (gs.x) {
-    const int G = gs.H / gs.g;
+  if (ex.x && ex.z) {
+    const uint16_t *xr = ex.x + (int64_t)t * ex.H;
+    const float acc = ex.zbits == 8 ? qgemv_row_wave<8>(xr, ex.H, ex.zw, ex.zs, ex.zb, ex.zgroup)
+                                    : qgemv_row_wave<4>(xr, ex.H, ex.zw, ex.zs, ex.zb, ex.zgroup);
+    if (lane == 0) ex.z[t] = (uint16_t)f2bf(acc);
+  }
+  if (ex.x && ex.xsum) {
+    const int G = ex.H / ex.g;
     for (int gi = lane; gi < G; gi += 64) {
-      const u32x4 *src = (const u32x4 *)(gs.x + (int64_t)t * gs.H + (int64_t)gi * gs.g);
-      u32x4 *dst = (u32x4 *)(gs.paired + (int64_t)t * gs.H + (int64_t)gi * gs.g);
-      gs.xsum[(int64_t)t * G + gi] = group_sum_paired(src, gs.g, dst);
+      const u32x4 *src = (const u32x4 *)(ex.x + (int64_t)t * ex.H + (int64_t)gi * ex.g);
+      u32x4 *dst = (u32x4 *)(ex.paired + (int64_t)t * ex.H + (int64_t)gi * ex.g);
+      ex.xsum[(int64_t)t * G + gi] = group_sum_paired(src, ex.g, dst);
     }
   }
 }
@@ -225,29 +232,31 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
 
 template <int KMAX>
 void launch_route_k(const uint16_t *logits, int T, int E, int k, int normalize, uint32_t *idx,
-                    uint16_t *scores, hipStream_t s, const RouteGroupSums &gs) {
+                    uint16_t *scores, hipStream_t s, const RouteExtras &ex) {
   const dim3 grid((T + 3) / 4), block(256);
   const int per = (E + 63) / 64;
   if (per <= 1)
-    hipLaunchKernelGGL((route_topk_kernel<1, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
+    hipLaunchKernelGGL((route_topk_kernel<1, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, ex);
   else if (per <= 2)
-    hipLaunchKernelGGL((route_topk_kernel<2, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
+    hipLaunchKernelGGL((route_topk_kernel<2, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, ex);
   else if (per <= 4)
-    hipLaunchKernelGGL((route_topk_kernel<4, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
+    hipLaunchKernelGGL((route_topk_kernel<4, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, ex);
   else if (per <= 8)
-    hipLaunchKernelGGL((route_topk_kernel<8, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
+    hipLaunchKernelGGL((route_topk_kernel<8, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, ex);
   else
-    hipLaunchKernelGGL((route_topk_kernel<16, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, gs);
+    hipLaunchKernelGGL((route_topk_kernel<16, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, ex);
 }
 
 hipError_t launch_route_topk(const uint16_t *logits, int T, int E, int k, int normalize,
-                             uint32_t *idx, uint16_t *scores, hipStream_t s, const RouteGroupSums &gs) {
+                             uint32_t *idx, uint16_t *scores, hipStream_t s, const RouteExtras &ex) {
   if (T <= 0) return hipSuccess;
-  if (gs.x && (gs.g <= 0 || gs.g % 8 || gs.H % gs.g || !gs.xsum || !gs.paired)) return hipErrorInvalidValue;
+  if (ex.x && ex.xsum && (ex.g <= 0 || ex.g % 8 || ex.H % ex.g || !ex.paired)) return hipErrorInvalidValue;
+  if (ex.x && ex.z && (ex.H % 32 || (ex.zbits != 4 && ex.zbits != 8) || ex.zgroup <= 0 || ex.zgroup % 32 || !ex.zw))
+    return hipErrorInvalidValue;
   // KMAX bounds the renormalisation's unrolled slice sum
-  if (k <= 8) launch_route_k<8>(logits, T, E, k, normalize, idx, scores, s, gs);
-  else if (k <= 16) launch_route_k<16>(logits, T, E, k, normalize, idx, scores, s, gs);
-  else launch_route_k<64>(logits, T, E, k, normalize, idx, scores, s, gs);
+  if (k <= 8) launch_route_k<8>(logits, T, E, k, normalize, idx, scores, s, ex);
+  else if (k <= 16) launch_route_k<16>(logits, T, E, k, normalize, idx, scores, s, ex);
+  else launch_route_k<64>(logits, T, E, k, normalize, idx, scores, s, ex);
   return hipGetLastError();
 }
 
