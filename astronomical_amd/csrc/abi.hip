@@ -115,8 +115,9 @@ struct Layout {
   int64_t act_ld;  // row length of act
 };
 
-// The decode path takes small batches: at most 8 tokens and 64 assignments, a dense router,
-// and shapes its per-lane register tiles cover (decode.hip: decode_supported).
+// The decode path takes small batches: at most 8 tokens and 64 assignments, a bf16 or affine
+// router, resident experts or a compact page, and shapes its per-lane register tiles cover
+// (decode.hip: decode_supported).
 // Leading dimension of the routed expert arrays: the expert count for resident weights, the
 // page's slot count for compact pages (slot_of_expert set).
 int expert_capacity(const astro_moe_layer &L) {
@@ -128,7 +129,7 @@ bool decode_path(const astro_moe_layer &L, int T) {
   const astro_moe_affine &gu = L.gate_up.w ? L.gate_up : L.gate;
   const bool router_ok = L.router_w ? true
                                     : (L.router_q.bits == 4 || L.router_q.bits == 8) && L.router_q.group_size >= 32;
-  return !L.slot_of_expert && T >= 1 && T <= 8 && T * L.top_k <= 64 && L.top_k <= kDecodeMaxK &&
+  return T >= 1 && T <= 8 && T * L.top_k <= 64 && L.top_k <= kDecodeMaxK &&
          router_ok && L.hidden <= 4096 &&
          L.intermediate <= 1024 && Is <= 1024 && (gu.bits == 4 || gu.bits == 8) &&
          (L.down.bits == 4 || L.down.bits == 8) &&
@@ -167,6 +168,8 @@ Layout block_layout(const astro_moe_layer &L, int T, int kk, bool with_router) {
     o.sparse = take((size_t)T * L.hidden * 2);
     o.shared_out = Is ? o.eout + A * (size_t)L.hidden * 2 : 0;
     o.z = take(Is ? (size_t)T * 2 : 0);
+    o.slots = take(L.slot_of_expert ? A * 4 : 0);
+    o.missing = take(L.slot_of_expert ? 4 : 0);
   } else {
     o.tile_expert = take((size_t)o.max_tiles * 4);
     o.tile_row0 = take((size_t)o.max_tiles * 4);
@@ -671,6 +674,15 @@ int run_block(const astro_moe_layer *layer, const uint16_t *x, int32_t tokens, u
       d.ffn_out = step->out;
     }
     d.unsorted = verification;
+    // compact pages: sorted by slot over every slot id (run_sparse's bucket count)
+    d.buckets = E;
+    if (L.slot_of_expert) {
+      d.slot_of_expert = L.slot_of_expert;
+      d.slots = (uint32_t *)at(o.slots);
+      d.missing = (uint32_t *)at(o.missing);
+      d.slot_count = expert_capacity(L);
+      d.buckets = std::max(E, d.slot_count);
+    }
     if (!decode_supported(d)) return fail(ASTRO_MOE_UNSUPPORTED, kBlockOp, "decode path geometry");
     // kernel-attached events: router | gate/up (shared gate/up, routing, sort inside) |
     // down (shared down and the combine inside)

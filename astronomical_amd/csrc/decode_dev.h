@@ -351,8 +351,19 @@ __global__ __launch_bounds__(256) void decode_router_kernel(const DecodeArgs p) 
 // ---------------------------------------------------------------- D2: route + gate/up
 
 // what decode_route writes to the workspace: the routing (ids, scores, sort, inverse, sorted
-// ids, offsets) and the distinct-expert table (count, expert / first row / rows, tokens)
+// ids, offsets; with a compact page also each assignment's slot and the missing count) and the
+// distinct-expert table (count, expert / first row / rows, tokens)
 constexpr int kPublishRoute = 1, kPublishTable = 2;
+
+// Where expert e's weights are: e itself, or its compact page slot (an expert with no slot, or
+// with a slot past the page, reads slot 0; absent tells the caller to count it).
+__device__ __forceinline__ uint32_t page_slot(const DecodeArgs &p, uint32_t e, bool &absent) {
+  absent = false;
+  if (!p.slot_of_expert) return e;
+  const uint32_t s = e < (uint32_t)p.E ? p.slot_of_expert[e] : 0xffffffffu;
+  absent = s >= (uint32_t)p.slot_count;
+  return absent ? 0u : s;
+}
 
 // Routing of the <= 8 tokens from their logits, the stable sort of the <= 64 assignments and
 // the table of distinct experts, into LDS; publish (kPublish* bits) selects what is also written
@@ -392,8 +403,10 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, int publish, u
   }
   __syncthreads();
   if (wave == 0) {
-    // stable sort by (expert, slot): rank = number of smaller keys
-    const uint32_t key = lane < A ? (idx_sh[lane] << 6) | (uint32_t)lane : 0xffffffffu;
+    // stable sort by (expert or page slot, assignment): rank = number of smaller keys
+    bool absent = false;
+    const uint32_t wslot = lane < A ? page_slot(p, idx_sh[lane], absent) : 0u;
+    const uint32_t key = lane < A ? (wslot << 6) | (uint32_t)lane : 0xffffffffu;
     key_sh[lane] = key;
     __builtin_amdgcn_wave_barrier();
     // the AMAX >= A keys in broadcast reads, issued before any comparison
@@ -429,7 +442,10 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, int publish, u
         p.sorted_order[rank] = (uint32_t)lane;
         p.inverse_order[lane] = rank;
         p.sorted_ids[rank] = key >> 6;
+        if (p.slots) p.slots[lane] = wslot;
       }
+      const uint64_t absent_lanes = __ballot(lane < A && absent);
+      if (p.missing && lane == 0) *p.missing = (uint32_t)__popcll(absent_lanes);
     }
     if (publish & kPublishTable) {
       if (start) {
@@ -456,12 +472,12 @@ __device__ __forceinline__ void decode_route(const DecodeArgs &p, int publish, u
   }
   __syncthreads();
   if (publish & kPublishRoute) {
-    // expert offsets [E+2] (E+1: trailing out-of-range bucket, empty here)
-    for (int e = threadIdx.x; e <= p.E + 1; e += (int)blockDim.x) {
+    // bucket offsets [buckets + 2] (buckets + 1: trailing out-of-range bucket, empty here)
+    for (int e = threadIdx.x; e <= p.buckets + 1; e += (int)blockDim.x) {
       uint32_t c = 0;
 #pragma unroll
       for (int i = 0; i < AMAX; ++i) c += (i < A) & (sid_sh[i] < (uint32_t)e);
-      p.offsets[e] = e <= p.E ? c : (uint32_t)A;
+      p.offsets[e] = e <= p.buckets ? c : (uint32_t)A;
     }
   }
 }
@@ -585,6 +601,24 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
       uint32_t eg = ids[0];
 #pragma unroll
       for (int i = 1; i < 8; ++i) eg = g == i ? ids[i] : eg;
+      if (p.slot_of_expert) {
+        // a compact page: the g-th of the k slots in (slot, id order) order, the sort's order
+        // up to the ties of absent experts (all slot 0, one token: equal rows)
+        const int ln = (int)(threadIdx.x & 63);
+        uint32_t mine = ids[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) mine = ln == i ? ids[i] : mine;
+        bool absent;
+        const uint32_t sl = ln < p.k ? page_slot(p, mine, absent) : 0xffffffffu;
+        int rank = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t si = (uint32_t)__builtin_amdgcn_readlane((int)sl, i);
+          rank += (i < p.k) && (si < sl || (si == sl && i < ln));
+        }
+        const uint64_t hit = __ballot(ln < p.k && rank == g);
+        eg = (uint32_t)__builtin_amdgcn_readlane((int)sl, (int)__ffsll((long long)hit) - 1);
+      }
       if ((threadIdx.x & 63) == 0) g_expert_sh[0] = eg;
     }
     __syncthreads();
@@ -671,7 +705,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   for (int i = 0; i < PW; ++i) {
     const int j = wave + 4 * i;
     const int a = t * p.k + (j < p.k ? j : 0);
-    e[i] = p.idx[a];
+    e[i] = p.slots ? p.slots[a] : p.idx[a];  // the weights' expert or page slot
     r[i] = p.inverse_order[a];
   }
   const uint32_t *wrow[PW];

@@ -201,6 +201,13 @@ struct DecodeArgs {
   uint16_t *r_out, *x_out, *ffn_out;
   // target-verification windows: the unsorted combine at every A (token-local rows)
   bool unsorted;
+  // compact pages (slot_of_expert set, [E]): an expert's weights are at its page slot, the
+  // assignments sort by slot (buckets: max(E, the page's slot count)); an expert with no slot
+  // (0xffffffff) reads slot 0 and is counted in *missing (remap_slots_kernel's rule); slots[a]
+  // = the slot of assignment a; a slot past the page (>= slot_count) is treated as absent
+  const uint32_t *slot_of_expert;
+  uint32_t *slots, *missing;
+  int buckets, slot_count;
 };
 // the router kernel keeps the T normalised rows in LDS: the decoder step fuses into the decode
 // kernels when T * H * 2 bytes fit

@@ -203,6 +203,7 @@ def main():
         extra = decoder_step(CF, DS, ops, torch, blocks, K, W)
         extra["c1_decode_batched"] = batched_decode(CF, DS, ops, torch, blocks, K, W)
         extra["c1_decode_affine_router"] = affine_router_decode(CF, DS, ops, torch, layers, K, W)
+        extra["c1_decode_paged"] = paged_decode(CF, ops, torch, layers, K, W)
         extra.update(other_configs(CF, DS, ops, torch, K, W, layers[0]))
         extra["verification_lm_head"] = verification_qmv(CF, DS, ops, torch)
 
@@ -548,6 +549,65 @@ def batched_decode(CF, DS, ops, torch, blocks, K, W, sizes=(2, 4, 8)):
         del g, x, y, ws
     log(f"batched decode: {json.dumps(out)}")
     return out
+
+
+def paged_decode(CF, ops, torch, layers, K, W):
+    """c1 decode B=1 with every layer's routed arrays as a compact page (paged_execution.rs:
+    98-139): the page holds all of the layer's experts in a seeded permuted slot order and the
+    block gets its slot map, so the decode kernels read each selected expert at its slot and
+    sort the assignments by slot."""
+    import copy
+    cfg = CF.C1
+    H, nL, E = cfg.hidden, len(layers), cfg.experts
+    blocks = []
+    for l, L in enumerate(layers):
+        gen = torch.Generator().manual_seed(cfg.seed * 1000 + l)
+        perm = torch.randperm(E, generator=gen).cuda()  # slot -> expert
+        slot_of = torch.empty(E, dtype=torch.int32, device="cuda")
+        slot_of[perm] = torch.arange(E, dtype=torch.int32, device="cuda")
+        Lp = copy.copy(L)
+        Lp.gate_up = L.gate_up.map(lambda a: a.index_select(0, perm))
+        Lp.down = L.down.map(lambda a: a.index_select(0, perm))
+        Lp.slot_of_expert = slot_of
+        blocks.append(ops.MoeBlock(Lp))
+    x = c1_tokens_device(cfg, nL)
+    y = torch.empty_like(x)
+    ws = torch.empty(blocks[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+
+    def step():
+        for l in range(nL):
+            blocks[l].forward(x[l], out=y[l], workspace=ws)
+    step()
+    torch.cuda.synchronize()
+    missing = blocks[-1].trace(1, workspace=ws)["missing_slots"]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(W):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(K):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / K / nL * 1000
+    credited = (cfg.top_k + 1) * cfg.page_bytes
+    gbs = credited / (us * 1e-6) / 1e9
+    out = {"workload": f"c1 decode B=1, routed arrays as compact pages (all {E} experts, permuted slots), "
+                       f"graph of {nL} layers",
+           "us_per_layer": round(us, 2), "tokens_per_s": round(1e6 / us, 1),
+           "achieved_GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "missing_slots": int(missing)}
+    log(f"paged decode: {json.dumps(out)}")
+    del blocks, g, x, y, ws
+    return out
+
+
+def c1_tokens_device(cfg, n, step=17):
+    from astronomical_amd import device_synthetic as DS
+    return DS.make_tokens_device(cfg, n, step=step).reshape(n, 1, cfg.hidden)
 
 
 def affine_router_decode(CF, DS, ops, torch, layers, K, W, bits=4):

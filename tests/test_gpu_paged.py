@@ -43,7 +43,9 @@ def _u32(a):
     return _u32_dev(a)
 
 
-@pytest.mark.parametrize("cfg,T", [(CF.C1, 128), (CF.C0, 16), (CF.C1, 4)])
+# T <= 8 at c1 takes the decode kernels (one token: the routed workgroups' own slot ranks; two:
+# the in-workgroup table; 4 and 8: the routing kernel's table), larger batches the sorted path
+@pytest.mark.parametrize("cfg,T", [(CF.C1, 128), (CF.C0, 16), (CF.C1, 1), (CF.C1, 2), (CF.C1, 4), (CF.C1, 8)])
 def test_paged_block(ops, orc, cfg, T):
     L = S.make_layer(cfg)
     x = S.make_tokens(cfg, T)
@@ -77,10 +79,11 @@ def test_paged_block(ops, orc, cfg, T):
     assert_bf16_close(tr["sparse"], sparse_ref, what + " sparse")
 
 
-def test_paged_block_missing_expert_counted(ops):
-    cfg = CF.C0
+@pytest.mark.parametrize("cfg,T", [(CF.C0, 16), (CF.C1, 1), (CF.C1, 4)])
+def test_paged_block_missing_expert_counted(ops, cfg, T):
+    """Experts absent from the page are counted (the sorted path's remap kernel, or the decode
+    kernels' routing publisher)."""
     L = S.make_layer(cfg)
-    T = 16
     x = S.make_tokens(cfg, T)
     res = ops.MoeBlock(ops.to_device(L))
     res(_bf(x))
