@@ -365,23 +365,57 @@ __device__ __forceinline__ void xq_tile(const GemmArgs &p, char *lds, int nblk, 
       }
     }
   } else {
+    // The wave's rows x RW columns go through LDS (row-major, the ring's space, free once every
+    // wave is past its last step) so that each lane stores 16-B pieces of a row: ten stores per
+    // lane of whole 128-B lines instead of NR * NBW * 4 two-byte stores.  A tile reaching past
+    // N, or an output that is not 16-B aligned, takes the element stores.
+    const int col0 = nblk * XQ_NT + half * NT + wave * RW;
+    // (the same for every wave of the workgroup: the barrier below is taken by all or none)
+    const bool vec = p.ldc % 8 == 0 && ((uintptr_t)p.C & 15) == 0 && nblk * XQ_NT + half * NT + NT <= p.N;
+    if (vec) {
+      constexpr int OSTR = RW + 8;  // elements per staged row (16-B aligned rows)
+      static_assert(XQ_W * XQ_MT * OSTR * 2 <= XQ_OW, "the staged outputs fit before the windows");
+      __syncthreads();  // every wave is done reading the ring and the group sums
+      uint16_t *ot = (uint16_t *)lds + wave * (XQ_MT * OSTR);
 #pragma unroll
-    for (int rb = 0; rb < NR; ++rb)
+      for (int rb = 0; rb < NR; ++rb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = rb * 16 + kq * 4 + i;
-        if (r >= rows) continue;
-        uint16_t *crow = p.C + (int64_t)(p.c_rows ? (int)p.c_rows[row0 + r] : row0 + r) * p.ldc;
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) {
-          const int col = nblk * XQ_NT + half * NT + wave * RW + nb * 16 + c16;
-          if (col < p.N) {
+          for (int nb = 0; nb < NBW; ++nb) {
             float v = acc[rb][nb][i];
-            if (EPI == kEpiBias) v = round_bf(v) + bf2f(p.bias[col]);
-            crow[col] = (uint16_t)f2bf(v);
+            if (EPI == kEpiBias) v = round_bf(v) + bf2f(p.bias[col0 + nb * 16 + c16]);
+            ot[(rb * 16 + kq * 4 + i) * OSTR + nb * 16 + c16] = (uint16_t)f2bf(v);
+          }
+      // the wave reads back its own writes: its LDS operations complete in order
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      constexpr int PR = RW / 8;  // 16-B pieces per row
+      for (int q = lane; q < rows * PR; q += 64) {
+        const int r = q / PR, c = q - r * PR;
+        const u32x4 v = *(const u32x4 *)(ot + r * OSTR + 8 * c);
+        uint16_t *crow = p.C + (int64_t)(p.c_rows ? (int)p.c_rows[row0 + r] : row0 + r) * p.ldc;
+        *(u32x4 *)(crow + col0 + 8 * c) = v;
+      }
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < NR; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = rb * 16 + kq * 4 + i;
+          if (r >= rows) continue;
+          uint16_t *crow = p.C + (int64_t)(p.c_rows ? (int)p.c_rows[row0 + r] : row0 + r) * p.ldc;
+#pragma unroll
+          for (int nb = 0; nb < NBW; ++nb) {
+            const int col = col0 + nb * 16 + c16;
+            if (col < p.N) {
+              float v = acc[rb][nb][i];
+              if (EPI == kEpiBias) v = round_bf(v) + bf2f(p.bias[col]);
+              crow[col] = (uint16_t)f2bf(v);
+            }
           }
         }
-      }
+    }
   }
 }
 
