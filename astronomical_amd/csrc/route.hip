@@ -9,25 +9,29 @@ namespace astro {
 namespace {
 
 // One wave per token (route_token_exact in route_dev.h: the slice in the order MLX's CPU
-// argpartition leaves it).  With ex.x set, the wave also does the token's share of the work
-// RouteExtras lists: its group sums and paired copy (group_sums_kernel's work, one lane per
-// group, the same order of additions) and its shared-expert gate (qgemv_row_wave, as
+// argpartition leaves it), four tokens per workgroup.  With ex.x set, waves 4..7 of the
+// workgroup (launched with 8) do the same tokens' share of the work RouteExtras lists, beside
+// the routing: their group sums and paired copies (group_sums_kernel's work, one lane per group,
+// the same order of additions) and their shared-expert gates (qgemv_row_wave, as
 // qgemv_rows_kernel), which then need no launches of their own.
 template <int PER, int KMAX>
-__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t *__restrict__ logits,
+__global__ __launch_bounds__(512) void route_topk_kernel(const uint16_t *__restrict__ logits,
                                                          int T, int E, int k, int normalize,
                                                          uint32_t *__restrict__ idx,
                                                          uint16_t *__restrict__ scores, const RouteExtras ex) {
   __shared__ __attribute__((aligned(16))) uint32_t sh[4][KMAX];
   __shared__ uint32_t sel[4][kSelectWords<PER>];  // per wave: keys, the partition's pair tables
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int t = blockIdx.x * 4 + wave;
+  const int t = blockIdx.x * 4 + (wave & 3);
   if (t >= T) return;
-  uint32_t my_idx, my_score;
-  route_token_exact<PER, KMAX>(logits + (int64_t)t * E, E, k, normalize, sel[wave], sh[wave], my_idx, my_score);
-  if (lane < k) {
-    idx[(int64_t)t * k + lane] = my_idx;
-    scores[(int64_t)t * k + lane] = (uint16_t)my_score;
+  if (wave < 4) {
+    uint32_t my_idx, my_score;
+    route_token_exact<PER, KMAX>(logits + (int64_t)t * E, E, k, normalize, sel[wave], sh[wave], my_idx, my_score);
+    if (lane < k) {
+      idx[(int64_t)t * k + lane] = my_idx;
+      scores[(int64_t)t * k + lane] = (uint16_t)my_score;
+    }
+    return;
   }
   if (ex.x && ex.z) {
     const uint16_t *xr = ex.x + (int64_t)t * ex.H;
@@ -233,7 +237,7 @@ __global__ __launch_bounds__(kChunk) void sort_place_kernel(
 template <int KMAX>
 void launch_route_k(const uint16_t *logits, int T, int E, int k, int normalize, uint32_t *idx,
                     uint16_t *scores, hipStream_t s, const RouteExtras &ex) {
-  const dim3 grid((T + 3) / 4), block(256);
+  const dim3 grid((T + 3) / 4), block(ex.x ? 512 : 256);  // waves 4..7: the extras
   const int per = (E + 63) / 64;
   if (per <= 1)
     hipLaunchKernelGGL((route_topk_kernel<1, KMAX>), grid, block, 0, s, logits, T, E, k, normalize, idx, scores, ex);
