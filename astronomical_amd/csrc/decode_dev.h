@@ -666,9 +666,10 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
 
 // ---------------------------------------------------------------- D3: down + combine
 
-// One workgroup of 4 waves per (4 R output rows, token).  The token's k experts and the
-// shared expert are P = kDecodeMaxK + 1 participant rows per output row; wave w computes
-// participants w, w+4, w+8.  Quarter q of a wave (one DPP row of 16 lanes) takes output rows
+// One workgroup of 4 waves per (4 R output rows, token).  The token's k experts and, in a
+// block with a shared expert (SH), the shared expert are P = kDecodeMaxK (+ 1) participant
+// rows per output row; wave w computes participants w, w+4 (and w+8 when SH: a block
+// without one loads two participants per wave, not three).  Quarter q of a wave (one DPP row of 16 lanes) takes output rows
 // (4x + q) R .. + R and its 16 lanes split the input chunks (lane l16 takes chunks l16,
 // l16+16, ...); a participant's activation chunk is loaded once for its R rows.  The rounded
 // participant values meet in LDS, where wave 0 forms the weighted combine (slot order) and the
@@ -676,14 +677,14 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
 // batches take R > 1: fewer, longer workgroups (every workgroup's dependent chain of index
 // and weight loads is paid once per R rows).  Branch-free: participants past k, or a missing
 // shared expert, reuse slot 0's rows and are masked out.
-template <int BITS, int NC, bool SORTED, int R>
+template <int BITS, int NC, bool SORTED, int R, bool SH>
 __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
-  constexpr int KM = kDecodeMaxK, P = KM + 1, PW = (P + 3) / 4;
+  constexpr int KM = kDecodeMaxK, P = SH ? KM + 1 : KM, PW = (P + 3) / 4;
   __shared__ float vals[4][R][4 * PW];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
   const int t = blockIdx.y, h0 = (blockIdx.x * 4 + q) * R;
-  const bool has_shared = p.Is > 0;
+  const bool has_shared = SH && p.Is > 0;
   // loads the combine needs, issued first (a missing shared expert reads a score instead)
   const uint16_t zbits = has_shared ? p.z[t] : p.scores[0];
   const int hc = h0 + (l16 < R ? l16 : 0);  // this lane's row in the combine
@@ -857,10 +858,14 @@ void launch_down_r(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   const dim3 grid(a.H / (4 * R), a.T);
   // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64; a verification
   // window keeps the unsorted one (resident_execution.rs:161-162)
-  if (a.A >= 64 && !a.unsorted)
-    launch_timed(decode_down_kernel<BITS, NC, true, R>, grid, s, ev, a);
-  else
-    launch_timed(decode_down_kernel<BITS, NC, false, R>, grid, s, ev, a);
+  const bool sorted = a.A >= 64 && !a.unsorted;
+  if (a.Is > 0) {
+    if (sorted) launch_timed(decode_down_kernel<BITS, NC, true, R, true>, grid, s, ev, a);
+    else launch_timed(decode_down_kernel<BITS, NC, false, R, true>, grid, s, ev, a);
+  } else {
+    if (sorted) launch_timed(decode_down_kernel<BITS, NC, true, R, false>, grid, s, ev, a);
+    else launch_timed(decode_down_kernel<BITS, NC, false, R, false>, grid, s, ev, a);
+  }
 }
 
 template <int BITS, int NC>

@@ -246,10 +246,6 @@ __device__ __forceinline__ void heap_adjust(uint32_t *b, int hole, int len, uint
   b[hole] = value;
 }
 
-// std::nth_element(a, a + nth, a + n) over the unique keys a[0, n) in LDS, as libstdc++ runs
-// it (see above).  One wave; n <= 64 * PER; pg and pl hold 32 * PER words each.  The heap
-// selection (reached only after 2 floor(log2 n) unbalanced partitions, i.e. adversarial keys)
-// runs on one lane.
 // One median-of-three Hoare partition of [f, l) (C chunks of 64 positions cover [f + 1, l));
 // returns cut.  Branch-free: lanes 0-3 fetch the three median candidates and a[f] in one
 // read, every store is unconditional (lanes with nothing to store write their own word of
@@ -315,86 +311,6 @@ __device__ __forceinline__ int hoare_step(uint32_t *a, uint32_t *pg, uint32_t *p
   for (int i = 0; i < C; ++i) dst[i] = *(left[i] ? pl + gr[i] : right[i] ? pg + (nl - 1 - lr[i]) : spare + lane);
 #pragma unroll
   for (int i = 0; i < C; ++i) *(left[i] || right[i] ? a + dst[i] : spare + lane) = key[i];
-  wave_lds_order();
-  return cut;
-}
-
-// std::nth_element(a, a + nth, a + n) over the unique keys a[0, n) in LDS, as libstdc++ runs
-// it (see above).  One wave; n <= 64 * PER; pg and pl hold 32 * PER words each.  The heap
-// selection (reached only after 2 floor(log2 n) unbalanced partitions, i.e. adversarial keys)
-// runs on one lane.
-// One median-of-three Hoare partition of [f, l) (C chunks of 64 positions cover [f + 1, l));
-// returns cut.
-template <int C>
-__device__ __forceinline__ int hoare_step(uint32_t *a, uint32_t *pg, uint32_t *pl, int f, int l, int nch) {
-  const int lane = (int)(threadIdx.x & 63);
-  // the median of a[f + 1], a[mid], a[l - 1] becomes the pivot at f (__move_median_to_first);
-  // its reads and the range's are issued together
-  const int mid = f + ((l - f) >> 1);
-  const uint32_t x = a[f + 1], y = a[mid], z = a[l - 1], o = a[f];
-  uint32_t key[C];
-#pragma unroll
-  for (int i = 0; i < C; ++i) {
-    const int p = f + 1 + lane + 64 * i;
-    key[i] = C == 1 || i < nch ? a[p < l ? p : l - 1] : 0u;
-  }
-  int pos;
-  uint32_t piv;
-  if (x < y) {
-    if (y < z) pos = mid, piv = y;
-    else if (x < z) pos = l - 1, piv = z;
-    else pos = f + 1, piv = x;
-  } else if (x < z) pos = f + 1, piv = x;
-  else if (y < z) pos = l - 1, piv = z;
-  else pos = mid, piv = y;
-  // ranks of the keys of [f + 1, l) above and below the pivot, counted from the left
-  int gr[C], lr[C];
-  bool gt[C], lt[C];
-  int ng = 0, nl = 0;
-#pragma unroll
-  for (int i = 0; i < C; ++i) {
-    const int p = f + 1 + lane + 64 * i;
-    const bool valid = (C == 1 || i < nch) && p < l;
-    const uint32_t kv = p == pos ? o : key[i];  // the swap of the median to f
-    key[i] = kv;
-    gt[i] = valid && kv > piv;
-    lt[i] = valid && kv < piv;
-    if (C == 1 || i < nch) {
-      const uint64_t bg = __ballot(gt[i]), bl = __ballot(lt[i]);
-      gr[i] = ng + lanes_below(bg);
-      lr[i] = nl + lanes_below(bl);
-      ng += __popcll(bg);
-      nl += __popcll(bl);
-    } else {
-      gr[i] = lr[i] = 0;
-    }
-  }
-  const int cut = f + 1 + nl;
-  if (lane == 0) {
-    a[f] = piv;
-    a[pos] = o;
-  }
-  // pair tables: position of the m-th key above the pivot left of cut, of the m-th key below
-  // it from the right at or after cut; then each moving key reads its partner's position
-  bool left[C], right[C];
-#pragma unroll
-  for (int i = 0; i < C; ++i) {
-    const int p = f + 1 + lane + 64 * i;
-    left[i] = gt[i] && p < cut;
-    right[i] = lt[i] && p >= cut;
-    if (left[i]) pg[gr[i]] = (uint32_t)p;
-    if (right[i]) pl[nl - 1 - lr[i]] = (uint32_t)p;
-  }
-  wave_lds_order();
-  uint32_t dst[C];
-#pragma unroll
-  for (int i = 0; i < C; ++i) {
-    const uint32_t *src = left[i] ? pl + gr[i] : right[i] ? pg + (nl - 1 - lr[i]) : pg;
-    dst[i] = C == 1 || i < nch ? *src : 0u;
-  }
-#pragma unroll
-  for (int i = 0; i < C; ++i)
-    if (left[i] || right[i]) a[dst[i]] = key[i];
   wave_lds_order();
   return cut;
 }

@@ -408,9 +408,19 @@ def test_block_c3_skewed_subset(ops, orc):
 
 
 def test_block_c4_8bit(ops, orc):
+    """8-bit g32 without a shared expert: T <= 8 takes the decode kernels (two participants per
+    down-kernel wave, two input chunks per lane), T = 64 the grouped GEMMs."""
     L = S.make_layer(CF.C4)
-    for T in (1, 64):
+    for T in (1, 2, 8, 64):
         _check_block(ops, orc, L, S.make_tokens(CF.C4, T), f"c4 T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 2, 8])
+def test_block_c0_decode(ops, orc, T):
+    """c0's shapes (4-bit, top-4 of 32, no shared expert) through the decode kernels: one, two
+    and four output rows per quarter-wave in the down kernel."""
+    L = S.make_layer(CF.C0)
+    _check_block(ops, orc, L, S.make_tokens(CF.C0, T), f"c0 T={T}")
 
 
 def test_fused_and_separate_gate_up_are_bit_identical(ops):
