@@ -6,7 +6,7 @@
 //       recomputed by every routed workgroup, then the routed gate/up GEMV + SwiGLU: one
 //       wave per (gate row, up row) pair of one selected expert, every token routed to it;
 //   D3  per token: down GEMV rows of its k experts and of the shared expert (16 lanes per
-//       row, the participants spread over 4 waves), then the weighted combine and the
+//       row, the participants spread over 3 or 4 waves), then the weighted combine and the
 //       shared expert's gated add.
 // Affine rows are read once per distinct expert with 16 B per lane loads.  4-bit codes are
 // turned into bf16 pairs (128 + q) with one and/or per pair and multiplied by
@@ -666,21 +666,25 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
 
 // ---------------------------------------------------------------- D3: down + combine
 
-// One workgroup of 4 waves per (4 R output rows, token).  The token's k experts and, in a
-// block with a shared expert (SH), the shared expert are P = kDecodeMaxK (+ 1) participant
-// rows per output row; wave w computes participants w, w+4 (and w+8 when SH: a block
-// without one loads two participants per wave, not three).  Quarter q of a wave (one DPP row of 16 lanes) takes output rows
-// (4x + q) R .. + R and its 16 lanes split the input chunks (lane l16 takes chunks l16,
+// One workgroup per (4 R output rows, token).  The token's k experts and, in a block with a
+// shared expert (SH), the shared expert are P = kDecodeMaxK (+ 1) participant rows per output
+// row, dealt to NW waves so that none loads a participant it masks out: with the shared
+// expert 3 waves of 3 (wave w: participants w, w+3, w+6), without it 4 waves of 2 (w, w+4).
+// Quarter q of a wave (one DPP row of 16 lanes) takes output rows (4x + q) R .. + R and its 16 lanes split the input chunks (lane l16 takes chunks l16,
 // l16+16, ...); a participant's activation chunk is loaded once for its R rows.  The rounded
 // participant values meet in LDS, where wave 0 forms the weighted combine (slot order) and the
 // shared expert's gated add, lane l16 < R of quarter q for row (4x + q) R + l16.  Larger
 // batches take R > 1: fewer, longer workgroups (every workgroup's dependent chain of index
 // and weight loads is paid once per R rows).  Branch-free: participants past k, or a missing
 // shared expert, reuse slot 0's rows and are masked out.
+// waves per down-kernel workgroup: 9 participants with a shared expert (3 x 3), else 8 (4 x 2)
+template <bool SH>
+constexpr int kDownWaves = SH ? 3 : 4;
+
 template <int BITS, int NC, bool SORTED, int R, bool SH>
-__global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
-  constexpr int KM = kDecodeMaxK, P = SH ? KM + 1 : KM, PW = (P + 3) / 4;
-  __shared__ float vals[4][R][4 * PW];
+__global__ __launch_bounds__(64 * kDownWaves<SH>) void decode_down_kernel(const DecodeArgs p) {
+  constexpr int KM = kDecodeMaxK, P = SH ? KM + 1 : KM, NW = kDownWaves<SH>, PW = (P + NW - 1) / NW;
+  __shared__ float vals[4][R][NW * PW];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
   const int t = blockIdx.y, h0 = (blockIdx.x * 4 + q) * R;
@@ -704,7 +708,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   uint32_t e[PW], r[PW];
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
-    const int j = wave + 4 * i;
+    const int j = wave + NW * i;
     const int a = t * p.k + (j < p.k ? j : 0);
     e[i] = p.slots ? p.slots[a] : p.idx[a];  // the weights' expert or page slot
     r[i] = p.inverse_order[a];
@@ -718,7 +722,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   bool live[PW];
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
-    const int j = wave + 4 * i;
+    const int j = wave + NW * i;
     const bool shared = j == KM && has_shared;
     live[i] = (j < KM && j < p.k) || shared;
     orow[i] = shared ? (uint32_t)(p.A + t) : r[i];
@@ -774,7 +778,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
     for (int rr = 0; rr < R; ++rr) {
       const float v = round_bf(row_sum(acc[i][rr]));
       if (l16 == rr) {
-        vals[q][rr][wave + 4 * i] = v;
+        vals[q][rr][wave + NW * i] = v;
         if (live[i]) p.down_out[(int64_t)orow[i] * p.H + h0 + rr] = (uint16_t)f2bf(v);
       }
     }
@@ -791,13 +795,13 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const DecodeArgs p) {
   if (p.ffn_out) p.ffn_out[(int64_t)t * p.H + hc] = (uint16_t)f2bf(bf2f(rbits) + bf2f(out));
 }
 
-// 256-thread launch; ev (nullable) = {start, stop} events recorded around the kernel itself
+// threads per workgroup (256 unless given); ev (nullable) = {start, stop} events recorded around the kernel itself
 template <typename Kernel>
-void launch_timed(Kernel kernel, dim3 grid, hipStream_t s, const hipEvent_t *ev, const DecodeArgs &a) {
+void launch_timed(Kernel kernel, dim3 grid, hipStream_t s, const hipEvent_t *ev, const DecodeArgs &a, int threads = 256) {
   if (ev)
-    hipExtLaunchKernelGGL(kernel, grid, dim3(256), 0, s, ev[0], ev[1], 0, a);
+    hipExtLaunchKernelGGL(kernel, grid, dim3(threads), 0, s, ev[0], ev[1], 0, a);
   else
-    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(kernel, grid, dim3(threads), 0, s, a);
 }
 
 template <int BITS, int MT, int NC, int PER, int RPW>
@@ -860,8 +864,8 @@ void launch_down_r(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
   // window keeps the unsorted one (resident_execution.rs:161-162)
   const bool sorted = a.A >= 64 && !a.unsorted;
   if (a.Is > 0) {
-    if (sorted) launch_timed(decode_down_kernel<BITS, NC, true, R, true>, grid, s, ev, a);
-    else launch_timed(decode_down_kernel<BITS, NC, false, R, true>, grid, s, ev, a);
+    if (sorted) launch_timed(decode_down_kernel<BITS, NC, true, R, true>, grid, s, ev, a, 64 * kDownWaves<true>);
+    else launch_timed(decode_down_kernel<BITS, NC, false, R, true>, grid, s, ev, a, 64 * kDownWaves<true>);
   } else {
     if (sorted) launch_timed(decode_down_kernel<BITS, NC, true, R, false>, grid, s, ev, a);
     else launch_timed(decode_down_kernel<BITS, NC, false, R, false>, grid, s, ev, a);
