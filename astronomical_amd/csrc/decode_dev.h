@@ -6,7 +6,7 @@
 //       recomputed by every routed workgroup, then the routed gate/up GEMV + SwiGLU: one
 //       wave per (gate row, up row) pair of one selected expert, every token routed to it;
 //   D3  per token: down GEMV rows of its k experts and of the shared expert (16 lanes per
-//       row, the participants spread over 3 or 4 waves), then the weighted combine and the
+//       row, the participants spread over 3 to 9 waves), then the weighted combine and the
 //       shared expert's gated add.
 // Affine rows are read once per distinct expert with 16 B per lane loads.  4-bit codes are
 // turned into bf16 pairs (128 + q) with one and/or per pair and multiplied by
@@ -668,8 +668,9 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
 
 // One workgroup per (4 R output rows, token).  The token's k experts and, in a block with a
 // shared expert (SH), the shared expert are P = kDecodeMaxK (+ 1) participant rows per output
-// row, dealt to NW waves so that none loads a participant it masks out: with the shared
-// expert 3 waves of 3 (wave w: participants w, w+3, w+6), without it 4 waves of 2 (w, w+4).
+// row, dealt to NW waves so that none loads a participant it masks out: one per wave up to
+// four tokens; beyond, with the shared expert 3 waves of 3 (wave w: participants w, w+3,
+// w+6), without it 4 waves of 2 (w, w+4).
 // Quarter q of a wave (one DPP row of 16 lanes) takes output rows (4x + q) R .. + R and its 16 lanes split the input chunks (lane l16 takes chunks l16,
 // l16+16, ...); a participant's activation chunk is loaded once for its R rows.  The rounded
 // participant values meet in LDS, where wave 0 forms the weighted combine (slot order) and the
@@ -677,13 +678,9 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(const DecodeArgs p)
 // batches take R > 1: fewer, longer workgroups (every workgroup's dependent chain of index
 // and weight loads is paid once per R rows).  Branch-free: participants past k, or a missing
 // shared expert, reuse slot 0's rows and are masked out.
-// waves per down-kernel workgroup: 9 participants with a shared expert (3 x 3), else 8 (4 x 2)
-template <bool SH>
-constexpr int kDownWaves = SH ? 3 : 4;
-
-template <int BITS, int NC, bool SORTED, int R, bool SH>
-__global__ __launch_bounds__(64 * kDownWaves<SH>) void decode_down_kernel(const DecodeArgs p) {
-  constexpr int KM = kDecodeMaxK, P = SH ? KM + 1 : KM, NW = kDownWaves<SH>, PW = (P + NW - 1) / NW;
+template <int BITS, int NC, bool SORTED, int R, bool SH, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_down_kernel(const DecodeArgs p) {
+  constexpr int KM = kDecodeMaxK, P = SH ? KM + 1 : KM, PW = (P + NW - 1) / NW;
   __shared__ float vals[4][R][NW * PW];
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
@@ -857,18 +854,25 @@ void launch_gate_up_nc(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev)
   else launch_gate_up_per<BITS, MT, NC, 16>(a, s, ev);
 }
 
+template <int BITS, int NC, int R, bool SH, int NW>
+void launch_down_w(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev, bool sorted) {
+  const dim3 grid(a.H / (4 * R), a.T);
+  if (sorted) launch_timed(decode_down_kernel<BITS, NC, true, R, SH, NW>, grid, s, ev, a, 64 * NW);
+  else launch_timed(decode_down_kernel<BITS, NC, false, R, SH, NW>, grid, s, ev, a, 64 * NW);
+}
+
 template <int BITS, int NC, int R>
 void launch_down_r(const DecodeArgs &a, hipStream_t s, const hipEvent_t *ev) {
-  const dim3 grid(a.H / (4 * R), a.T);
   // routing.rs:13 / resident_execution.rs:86-95: sorted reduction iff A >= 64; a verification
   // window keeps the unsorted one (resident_execution.rs:161-162)
-  const bool sorted = a.A >= 64 && !a.unsorted;
+  // one wave per participant up to kDecodeDownWideT tokens, then 3 waves of 3 (4 of 2)
+  const bool sorted = a.A >= 64 && !a.unsorted, wide = a.T <= kDecodeDownWideT;
   if (a.Is > 0) {
-    if (sorted) launch_timed(decode_down_kernel<BITS, NC, true, R, true>, grid, s, ev, a, 64 * kDownWaves<true>);
-    else launch_timed(decode_down_kernel<BITS, NC, false, R, true>, grid, s, ev, a, 64 * kDownWaves<true>);
+    if (wide) launch_down_w<BITS, NC, R, true, 9>(a, s, ev, sorted);
+    else launch_down_w<BITS, NC, R, true, 3>(a, s, ev, sorted);
   } else {
-    if (sorted) launch_timed(decode_down_kernel<BITS, NC, true, R, false>, grid, s, ev, a);
-    else launch_timed(decode_down_kernel<BITS, NC, false, R, false>, grid, s, ev, a);
+    if (wide) launch_down_w<BITS, NC, R, false, 8>(a, s, ev, sorted);
+    else launch_down_w<BITS, NC, R, false, 4>(a, s, ev, sorted);
   }
 }
 

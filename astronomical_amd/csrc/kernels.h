@@ -224,6 +224,9 @@ constexpr int kDecodeMaxK = 8;         // experts per token the decode combine u
 // kDecodeDownR2T, then 4
 constexpr int kDecodeDownR1T = 1;
 constexpr int kDecodeDownR2T = 2;
+// the down kernel's workgroup takes one wave per participant up to this many tokens (c1: B = 1
+// 17.0 -> 16.3, B = 4 33.3 -> 31.2 us per layer), then 3 waves of 3 (B = 8: 48.1 against 49.4)
+constexpr int kDecodeDownWideT = 4;
 // tokens per pass of a gate/up wave of several row pairs (fewer registers, more waves per SIMD)
 constexpr int kDecodePassTokens = 2;
 // launches the decode kernels (router | [routing, T >= kDecodeRouteOnceT] | shared gate/up +
